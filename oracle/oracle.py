@@ -1,0 +1,619 @@
+"""CPU oracle for the NeuralScript emitted runtime (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
+import this module, and only as the checker; the product (libnship) never
+does.  It drives ``libns_oracle.so`` (ns_oracle.c, the bit-faithful kernel
+restatement) in the order the reference's emitted C++ runs them:
+
+* inference: ``gen_cpu`` forward body, /root/reference/src/codegen/codegen.cpp:1961-2288
+* training:  ``emit_train_core``, codegen.cpp:2659-3158 (forward body, then
+  reverse body, then the optimizer body, then the loss), wrapped as
+  ``ns_runtime_train_step`` at codegen.cpp:2636-2644.
+
+The network comes in as the text of ``nsc <net> --mlir``
+(mlir_compiler.cpp:949-1025); this module parses it independently of the
+product's C++ parser.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from dataclasses import dataclass, field
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libns_oracle.so")
+
+ACT_CODES = {"identity": 0, "relu": 1, "leaky_relu": 2, "sigmoid": 3, "tanh": 4,
+             "swish": 5, "silu": 5, "gelu": 6}
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_lib = None
+
+
+def build_command():
+    src = os.path.join(_HERE, "ns_oracle.c")
+    # -ffp-contract=off: the reference's emitted code never fuses a multiply
+    # and an add (g++ -O2 -std=c++11 on x86-64 has no FMA), so neither may we.
+    return ["gcc", "-O3", "-march=x86-64-v2", "-ffp-contract=off", "-fno-fast-math",
+            "-fopenmp", "-fPIC", "-shared", src, "-o", LIB_PATH, "-lm"]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        i64, sz, ci, cf = ctypes.c_int64, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+        sig = {
+            "or_act": (None, [_f32p, _f32p, sz, ci]),
+            "or_act_grad": (None, [_f32p, _f32p, _f32p, sz, ci]),
+            "or_matmul": (None, [_f32p, _f32p, _f32p, i64, i64, i64, ci]),
+            "or_matmul_rows": (None, [_f32p, _i64p, i64, _f32p, _f32p, i64, i64, ci]),
+            "or_matmul_grad_a": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
+            "or_matmul_grad_w": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
+            "or_layernorm": (None, [_f32p, _f32p, sz, i64]),
+            "or_layernorm_grad": (None, [_f32p, _f32p, _f32p, sz, i64]),
+            "or_embedding": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
+            "or_embedding_rows": (None, [_f32p, _i64p, i64, i64]),
+            "or_embedding_grad_w": (None, [_f32p, _f32p, _f32p, sz, i64, i64]),
+            "or_cross_entropy": (cf, [_f32p, _f32p, sz, i64]),
+            "or_loss_grad": (None, [_f32p, _f32p, _f32p, sz, i64]),
+            "or_attention_fwd": (None, [_f32p] * 6 + [i64, i64, i64]),
+            "or_attention_fwd_rows": (None, [_f32p] * 5 + [_i64p, i64, _f32p, i64, i64, i64]),
+            "or_attention_bwd": (None, [_f32p] * 11 + [i64, i64, i64]),
+            "or_moe_gate_logits": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
+            "or_moe_fwd": (None, [_f32p] * 4 + [_u8p, _f32p, _i64p, _f32p, i64, i64, i64, i64]),
+            "or_moe_bwd": (None, [_f32p] * 5 + [_u8p] + [_f32p] * 4 + [i64, i64, i64, i64]),
+            "or_orthonom": (None, [_f32p, i64, i64]),
+            "or_muon_step": (None, [_f32p, _f32p, i64, i64, cf]),
+            "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, sz, i64, cf]),
+            "or_use_muon": (ci, [i64, i64]),
+            "or_lr_scale_cosine": (cf, [i64]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def fp(a):
+    """float32 pointer of a C-contiguous float32 array (None -> NULL)."""
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_f32p)
+
+
+def ip(a):
+    if a is None:
+        return None
+    assert a.dtype == np.int64 and a.flags.c_contiguous
+    return a.ctypes.data_as(_i64p)
+
+
+def up(a):
+    if a is None:
+        return None
+    assert a.dtype == np.uint8 and a.flags.c_contiguous
+    return a.ctypes.data_as(_u8p)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def empty(n):
+    return np.empty(int(n), dtype=np.float32)
+
+
+# ---------------------------------------------------------------------------
+# kernel wrappers (flat float32 arrays in, flat arrays out)
+# ---------------------------------------------------------------------------
+
+def matmul(A, B, M, K, N, act=0):
+    C = empty(M * N)
+    lib().or_matmul(fp(A), fp(B), fp(C), M, K, N, act)
+    return C
+
+
+def matmul_rows(A, rows, B, K, N, act=0):
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    C = empty(len(rows) * N)
+    lib().or_matmul_rows(fp(A), ip(rows), len(rows), fp(B), fp(C), K, N, act)
+    return C
+
+
+def act(x, code):
+    y = empty(x.size)
+    lib().or_act(fp(x), fp(y), x.size, code)
+    return y
+
+
+def act_grad(din, pre, code):
+    y = empty(din.size)
+    lib().or_act_grad(fp(din), fp(pre), fp(y), din.size, code)
+    return y
+
+
+def matmul_grad_a(dC, B, M, K, N):
+    dA = empty(M * K)
+    lib().or_matmul_grad_a(fp(dC), fp(B), fp(dA), M, K, N)
+    return dA
+
+
+def matmul_grad_w(A, dC, M, K, N):
+    dB = empty(K * N)
+    lib().or_matmul_grad_w(fp(A), fp(dC), fp(dB), M, K, N)
+    return dB
+
+
+def layernorm(x, last):
+    y = empty(x.size)
+    lib().or_layernorm(fp(x), fp(y), x.size, last)
+    return y
+
+
+def layernorm_grad(dout, x, last):
+    y = empty(dout.size)
+    lib().or_layernorm_grad(fp(dout), fp(x), fp(y), dout.size, last)
+    return y
+
+
+def embedding(W, idx, V, D):
+    out = empty(idx.size * D)
+    lib().or_embedding(fp(W), fp(idx), fp(out), idx.size, V, D)
+    return out
+
+
+def embedding_rows(idx, V):
+    rows = np.empty(idx.size, dtype=np.int64)
+    lib().or_embedding_rows(fp(idx), ip(rows), idx.size, V)
+    return rows
+
+
+def embedding_grad_w(dout, idx, V, D):
+    dW = empty(V * D)
+    lib().or_embedding_grad_w(fp(dout), fp(idx), fp(dW), dout.size // D, D, V)
+    return dW
+
+
+def cross_entropy(preds, labels, C):
+    return float(lib().or_cross_entropy(fp(preds), fp(labels), preds.size, C))
+
+
+def loss_grad(preds, labels, C):
+    d = empty(preds.size)
+    lib().or_loss_grad(fp(preds), fp(labels), fp(d), preds.size, C)
+    return d
+
+
+def attention_fwd(x, Wq, Wk, Wv, Wo, BS, D, H):
+    out = empty(BS * D)
+    lib().or_attention_fwd(fp(x), fp(Wq), fp(Wk), fp(Wv), fp(Wo), fp(out), BS, D, H)
+    return out
+
+
+def attention_fwd_rows(x, Wq, Wk, Wv, Wo, rows, BS, D, H):
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    out = empty(len(rows) * D)
+    lib().or_attention_fwd_rows(fp(x), fp(Wq), fp(Wk), fp(Wv), fp(Wo), ip(rows), len(rows),
+                                fp(out), BS, D, H)
+    return out
+
+
+def attention_bwd(dout, x, Wq, Wk, Wv, Wo, BS, D, H):
+    dX, dWq, dWk, dWv, dWo = empty(BS * D), empty(D * D), empty(D * D), empty(D * D), empty(D * D)
+    lib().or_attention_bwd(fp(dout), fp(x), fp(Wq), fp(Wk), fp(Wv), fp(Wo), fp(dX), fp(dWq),
+                           fp(dWk), fp(dWv), fp(dWo), BS, D, H)
+    return dX, dWq, dWk, dWv, dWo
+
+
+def moe_gate_logits(x, Wg, M, D, E):
+    lg = empty(M * E)
+    lib().or_moe_gate_logits(fp(x), fp(Wg), fp(lg), M, D, E)
+    return lg
+
+
+def moe_fwd(x, Wg, We1, We2, active, M, D, H, E):
+    out = empty(M * D)
+    best = np.empty(M, dtype=np.int64)
+    prob = empty(M)
+    lib().or_moe_fwd(fp(x), fp(Wg), fp(We1), fp(We2), up(active), fp(out), ip(best), fp(prob),
+                     M, D, H, E)
+    return out, best, prob
+
+
+def moe_bwd(dout, x, Wg, We1, We2, active, M, D, H, E):
+    dx, dWg, dWe1, dWe2 = empty(M * D), empty(D * E), empty(E * D * H), empty(E * H * D)
+    lib().or_moe_bwd(fp(dout), fp(x), fp(Wg), fp(We1), fp(We2), up(active), fp(dx), fp(dWg),
+                     fp(dWe1), fp(dWe2), M, D, H, E)
+    return dx, dWg, dWe1, dWe2
+
+
+def orthonom(G, M, N):
+    G = f32(G).copy()
+    lib().or_orthonom(fp(G), M, N)
+    return G
+
+
+def use_muon(r, c):
+    return bool(lib().or_use_muon(r, c))
+
+
+def lr_scale_cosine(step):
+    return float(lib().or_lr_scale_cosine(step))
+
+
+# ---------------------------------------------------------------------------
+# IR text (nsc --mlir) parsing
+# ---------------------------------------------------------------------------
+
+_LINE = re.compile(r"^\s*(ns\.[\w.]+)((?:\s+%[\w.]+)*)\s*(?::\s*Tensor\[([^\]]*)\][^/]*)?(?://\s?(.*))?$")
+
+
+@dataclass
+class Instr:
+    op: str
+    result: str | None
+    operands: list
+    dims: list | None
+    comment: str
+
+
+@dataclass
+class Func:
+    name: str
+    instrs: list = field(default_factory=list)
+    ret: str | None = None
+
+    @property
+    def is_train(self):
+        return any(i.op == "ns.grad" for i in self.instrs)
+
+
+_NO_RESULT = {"ns.grad", "ns.opt.step", "ns.forward"}
+
+
+def parse_ir(text):
+    funcs, cur = [], None
+    for raw in text.splitlines():
+        line = raw.strip()
+        if not line or line.startswith("//"):
+            continue
+        if line.startswith("ns.func @"):
+            cur = Func(line[len("ns.func @"):].split()[0])
+            funcs.append(cur)
+            continue
+        if line == "}":
+            cur = None
+            continue
+        if line.startswith("ns.return"):
+            cur.ret = line.split("%", 1)[1].strip()
+            continue
+        m = _LINE.match(line)
+        if not m:
+            raise ValueError(f"unparsed IR line: {raw!r}")
+        op, ids, dims, comment = m.group(1), m.group(2), m.group(3), m.group(4) or ""
+        names = [t[1:] for t in ids.split()]
+        if op in _NO_RESULT:
+            res, opnds = None, names
+        else:
+            res, opnds = (names[0] if names else None), names[1:]
+        dl = None
+        if dims is not None:
+            dl = []
+            for d in dims.split(","):
+                d = d.strip()
+                dl.append(int(d) if d.lstrip("-").isdigit() else -1)
+        cur.instrs.append(Instr(op, res, opnds, dl, comment.strip()))
+    return funcs
+
+
+def comment_attr(comment, key):
+    m = re.search(r"\b%s=(\d+)" % key, comment)
+    return int(m.group(1)) if m else None
+
+
+class Net:
+    """Static facts of a network: weights in TENSOR_ALLOC order, geometry."""
+
+    def __init__(self, ir_text):
+        self.funcs = parse_ir(ir_text)
+        self.fwd = next((f for f in self.funcs if not f.is_train), None)
+        self.train = next((f for f in self.funcs if f.is_train), None)
+        if self.fwd is None:
+            raise ValueError("IR has no forward function")
+        self.weights = []  # (name, rows, cols)
+        for i in self.fwd.instrs:
+            if i.op == "ns.tensor.alloc":
+                r = i.dims[0] if len(i.dims) > 0 else 1
+                c = i.dims[1] if len(i.dims) > 1 else 1
+                self.weights.append((i.result, r, c))
+        self.shape = {n: (r, c) for n, r, c in self.weights}
+        self.offsets, off = {}, 0
+        for n, r, c in self.weights:
+            self.offsets[n] = off
+            off += r * c
+        self.total = off
+        # attention heads and MoE geometry, keyed by the first weight operand
+        self.heads, self.moe = {}, None
+        for f in self.funcs:
+            for i in f.instrs:
+                if i.op == "ns.layer.attention":
+                    self.heads[i.operands[1]] = comment_attr(i.comment, "heads") or 1
+                if i.op == "ns.layer.moe":
+                    D, E = self.shape[i.operands[1]]
+                    H = self.shape[i.operands[2]][1] // D
+                    k0 = comment_attr(i.comment, "initial") or E
+                    if k0 <= 0 or k0 > E:
+                        k0 = E
+                    self.moe = dict(D=D, E=E, H=H, K0=k0, g=i.operands[1])
+        self.in_cols, self.out_cols = self._geometry()
+
+    def _rt_cols(self, f, vid):
+        for i in f.instrs:
+            if i.result == vid and i.dims and len(i.dims) > 1:
+                return i.dims[1]
+        if vid in self.shape:
+            return self.shape[vid][1]
+        return -1
+
+    def _geometry(self):
+        """in_cols / out_cols as the emitted driver computes them
+        (codegen.cpp:2295-2320)."""
+        f = self.fwd
+        in_cols = out_cols = -1
+        for i in f.instrs:
+            if i.op != "ns.tensor.alloc" and i.result and i.result == f.ret:
+                out_cols = self._rt_cols(f, i.result)
+        for i in f.instrs:
+            if i.op == "ns.matmul" and len(i.operands) >= 2:
+                if in_cols < 0:
+                    in_cols = self.shape[i.operands[1]][0]
+                out_cols = self.shape[i.operands[1]][1]
+            if i.op == "ns.layer.embedding" and in_cols < 0:
+                in_cols = 1
+            if i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe") and i.result:
+                c = self._rt_cols(f, i.result)
+                if c > 0:
+                    out_cols = c
+        return (in_cols if in_cols > 0 else 1), (out_cols if out_cols > 0 else 1)
+
+    def output_numel(self, input_numel):
+        return (input_numel // self.in_cols) * self.out_cols
+
+
+def _act_of(f, pre):
+    for i in f.instrs:
+        if i.op.startswith("ns.activation.") and i.operands and i.operands[0] == pre:
+            return ACT_CODES[i.op.split(".")[-1]]
+    raise ValueError(f"no activation consumes {pre}")
+
+
+def _input_id(f, weights):
+    for i in f.instrs:
+        if i.op == "ns.layer.embedding" and len(i.operands) >= 2:
+            return i.operands[1]
+        if i.op == "ns.matmul" and i.operands and i.operands[0] not in weights:
+            return i.operands[0]
+        if i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe", "ns.dropout") or \
+                i.op.startswith("ns.activation."):
+            if i.operands and i.operands[0] not in weights:
+                return i.operands[0]
+    return None
+
+
+class Model:
+    """One model instance: blob, MoE liveness, optimizer state, LR step."""
+
+    def __init__(self, net: Net, weights):
+        w = f32(weights).ravel()
+        if w.size != net.total:
+            raise ValueError("weight count mismatch")
+        self.net = net
+        self.w = w.copy()
+        self.lr_step = 0
+        self.adam = {}  # name -> (m, v, t)
+        self.active = None
+        if net.moe:
+            self.active = np.zeros(net.moe["E"], dtype=np.uint8)
+            self.active[: net.moe["K0"]] = 1
+
+    def weight(self, name):
+        r, c = self.net.shape[name]
+        o = self.net.offsets[name]
+        return self.w[o:o + r * c]
+
+    # -- shared op semantics ------------------------------------------------
+    def _run(self, f, x, y, train_mode, record=None):
+        net = self.net
+        wset = set(net.shape)
+        buf = {}
+        xid = _input_id(f, wset)
+        yid = None
+        for i in f.instrs:
+            if i.op == "ns.cross_entropy":
+                yid = i.operands[1]
+
+        def val(v):
+            if v == xid:
+                return x
+            if v == yid:
+                return y
+            if v in wset:
+                return self.weight(v)
+            return buf[v]
+
+        width = {}
+
+        def cols(v):
+            if v in width:
+                return width[v]
+            if v in wset:
+                return net.shape[v][1]
+            if v == xid:
+                return net.in_cols
+            return -1
+
+        grads = {}
+        loss = None
+        for i in f.instrs:
+            op, o = i.op, i.operands
+            if op in ("ns.tensor.alloc", "ns.grad", "ns.forward"):
+                continue
+            if op == "ns.matmul":
+                A = val(o[0])
+                K, N = net.shape[o[1]]
+                M = A.size // K
+                buf[i.result] = matmul(A, val(o[1]), M, K, N)
+                width[i.result] = N
+            elif op.startswith("ns.activation."):
+                kind = op.split(".")[-1]
+                if kind not in ACT_CODES:
+                    raise NotImplementedError(op)
+                buf[i.result] = act(val(o[0]), ACT_CODES[kind])
+                width[i.result] = cols(o[0])
+            elif op == "ns.dropout":
+                if train_mode:
+                    raise NotImplementedError("dropout in training draws from mt19937")
+                buf[i.result] = val(o[0]).copy()
+                width[i.result] = cols(o[0])
+            elif op == "ns.layernorm":
+                src = val(o[0])
+                last = i.dims[1] if (i.dims and len(i.dims) > 1 and i.dims[1] > 0) else cols(o[0])
+                if f.is_train:
+                    last = cols(o[0]) if cols(o[0]) > 0 else last
+                buf[i.result] = layernorm(src, max(last, 1))
+                width[i.result] = last
+            elif op == "ns.layer.embedding":
+                V, D = net.shape[o[0]]
+                buf[i.result] = embedding(val(o[0]), val(o[1]), V, D)
+                width[i.result] = D
+            elif op == "ns.layer.attention":
+                D = net.shape[o[1]][0]
+                H = net.heads[o[1]]
+                xa = val(o[0])
+                BS = xa.size // D
+                buf[i.result] = attention_fwd(xa, *(val(w) for w in o[1:5]), BS, D, H)
+                width[i.result] = D
+            elif op == "ns.layer.moe":
+                m = net.moe
+                xa = val(o[0])
+                M = xa.size // m["D"]
+                out, best, prob = moe_fwd(xa, *(val(w) for w in o[1:4]), self.active,
+                                          M, m["D"], m["H"], m["E"])
+                buf[i.result] = out
+                width[i.result] = m["D"]
+                if record is not None:
+                    record["moe_best"] = best
+                    record["moe_prob"] = prob
+            elif op == "ns.cross_entropy":
+                C = cols(o[0])
+                loss = cross_entropy(val(o[0]), y, C)
+            elif not train_mode:
+                continue
+            elif op == "ns.grad.loss":
+                C = cols(o[0])
+                buf[i.result] = loss_grad(val(o[0]), y, C)
+                width[i.result] = C
+            elif op == "ns.grad.matmul.a":
+                dC = val(o[0])
+                K, N = net.shape[o[1]]
+                M = dC.size // N
+                buf[i.result] = matmul_grad_a(dC, val(o[1]), M, K, N)
+                width[i.result] = K
+            elif op == "ns.grad.matmul.w":
+                dC = val(o[1])
+                K, N = net.shape[o[2]]
+                M = dC.size // N
+                buf[i.result] = matmul_grad_w(val(o[0]), dC, M, K, N)
+                grads[o[2]] = i.result
+            elif op == "ns.grad.activation":
+                code = _act_of(f, o[1])
+                buf[i.result] = act_grad(val(o[0]), val(o[1]), code)
+                width[i.result] = cols(o[0])
+            elif op == "ns.grad.layernorm":
+                last = cols(o[1])
+                buf[i.result] = layernorm_grad(val(o[0]), val(o[1]), max(last, 1))
+                width[i.result] = last
+            elif op == "ns.grad.embedding.w":
+                V, D = net.shape[o[2]]
+                buf[i.result] = embedding_grad_w(val(o[0]), val(o[1]), V, D)
+            elif op.startswith("ns.grad.attention."):
+                which = op.split(".")[-1]
+                key = ("attn", o[0], o[1], o[2])
+                if key not in buf:
+                    D = net.shape[o[2]][0]
+                    H = net.heads[o[2]]
+                    dout = val(o[0])
+                    BS = dout.size // D
+                    buf[key] = attention_bwd(dout, val(o[1]), *(val(w) for w in o[2:6]), BS, D, H)
+                idx = {"x": 0, "wq": 1, "wk": 2, "wv": 3, "wo": 4}[which]
+                buf[i.result] = buf[key][idx]
+                if which == "x":
+                    width[i.result] = net.shape[o[2]][0]
+            elif op.startswith("ns.grad.moe."):
+                which = op.split(".")[-1]
+                key = ("moe", o[0], o[1])
+                m = net.moe
+                if key not in buf:
+                    dout = val(o[0])
+                    M = dout.size // m["D"]
+                    buf[key] = moe_bwd(dout, val(o[1]), *(val(w) for w in o[2:5]), self.active,
+                                       M, m["D"], m["H"], m["E"])
+                idx = {"x": 0, "wg": 1, "we1": 2, "we2": 3}[which]
+                buf[i.result] = buf[key][idx]
+                if which == "x":
+                    width[i.result] = m["D"]
+            elif op == "ns.opt.step":
+                self._opt_step(o, val, record)
+            else:
+                raise NotImplementedError(op)
+        if record is not None:
+            record["buf"] = buf
+        return buf, loss
+
+    def _opt_step(self, o, val, record):
+        """codegen.cpp:3088-3124, pairs in TENSOR_ALLOC order."""
+        lr = self._lr
+        L = lib()
+        for k in range(0, len(o) - 1, 2):
+            name, g = o[k], o[k + 1]
+            r, c = self.net.shape[name]
+            w = self.weight(name)  # view into the blob: updated in place
+            gr = f32(val(g)).copy()
+            if use_muon(r, c):
+                L.or_muon_step(fp(w), fp(gr), r, c, ctypes.c_float(lr))
+            else:
+                m, v, t = self.adam.get(name, (np.zeros(r * c, np.float32),
+                                               np.zeros(r * c, np.float32), 0))
+                t += 1
+                L.or_adamw_step(fp(w), fp(gr), fp(m), fp(v), r * c, t, ctypes.c_float(lr))
+                self.adam[name] = (m, v, t)
+
+    # -- C-ABI mirror -------------------------------------------------------
+    def eval_infer(self, x, record=None):
+        x = f32(x).ravel()
+        buf, _ = self._run(self.net.fwd, x, None, False, record)
+        return buf[self.net.fwd.ret].copy()
+
+    def train_step(self, x, labels, lr, record=None):
+        """ns_runtime_train_step with the compiled-in constant schedule
+        (multiplier 1.0, codegen.cpp:2639-2642)."""
+        self.lr_step += 1
+        self._lr = np.float32(lr) * np.float32(1.0)
+        _, loss = self._run(self.net.train, f32(x).ravel(), f32(labels).ravel(), True, record)
+        return np.float32(loss)
+
+    def objective_loss(self, x, labels):
+        self._lr = np.float32(0.0)
+        _, loss = self._run(self.net.train, f32(x).ravel(), f32(labels).ravel(), False)
+        return np.float32(loss)
