@@ -1,0 +1,168 @@
+"""Benchmark of the NeuralScript HIP backend on one MI355X.
+
+Default workload = BASELINE.json configs[1] (c2): ns_eval_infer forward of the
+fp32 MLP 1024->4096 GELU->4096 GELU->1024 at batch 8192, inputs already in
+HBM (nsh_eval_infer_device), synthetic data / seeded weights.  One "step" is
+one forward pass over the 8192-row batch.
+
+Prints ONE JSON line with the driver's contract plus
+  roofline     -- the dominant kernel (fp32-MFMA GEMM): algorithmic FLOP per
+                  launch / average launch time from HIP events recorded on the
+                  model's stream around every launch in the timed region;
+  cpu_baseline -- the reference CPU path (the driver the reference compiler
+                  emits, built from its sources into oracle/_ref) on a bounded
+                  sample of the same workload, 1 core; the oracle port when
+                  that build is absent.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "ns_eval_infer tokens/s + % of fp32-MFMA/HBM roofline; train steps/s"
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+HBM_PEAK_GBS = 8000.0
+
+
+def c2_flops(rows):
+    return 2.0 * rows * (1024 * 4096 + 4096 * 4096 + 4096 * 1024)
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), if any."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get(kernel)
+
+
+def cpu_baseline_c2(budget_s=12.0):
+    """Reference CPU driver (nsc --cpp --runtime, g++ -O2) on a row sample."""
+    from neuralscript_amd import runtime, workloads
+    from neuralscript_amd.abi import NsLib
+    ref = os.path.join(ROOT, "oracle", "_ref", "libc2.so")
+    plan = runtime.Plan.load("c2")
+    shapes = workloads.ir_shapes(plan.ir)
+    w = workloads.weights("c2", plan.layout(), shapes)
+    if os.path.exists(ref):
+        kind = "reference"
+        lib = NsLib(ref)
+        m = lib.init(w)
+        run = lambda x: lib.eval_infer(m, x)  # noqa: E731
+        done = lambda: lib.free(m)  # noqa: E731
+    else:
+        kind = "port"
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        os.environ.setdefault("OMP_NUM_THREADS", "1")
+        om = oracle.Model(oracle.Net(plan.ir), w)
+        run = om.eval_infer
+        done = lambda: None  # noqa: E731
+    x_all = workloads.inputs("c2", rows=64)
+    t0 = time.perf_counter()
+    run(x_all[:1024])                     # 1 row: calibrates the sample size
+    t1 = time.perf_counter() - t0
+    rows = int(max(1, min(64, budget_s / max(t1, 1e-3))))
+    t0 = time.perf_counter()
+    run(x_all[: rows * 1024])
+    dt = time.perf_counter() - t0
+    done()
+    return {"value": rows / dt, "unit": "tokens/s", "cores": 1, "kind": kind,
+            "sample": f"c2 forward on {rows} of the 8192 rows (same weights/inputs), "
+                      f"{dt:.1f} s, single-threaded as the reference emits it"}
+
+
+def bench_c2(steps, warmup, with_cpu):
+    from neuralscript_amd import runtime, workloads
+    if not runtime.has_gpu():
+        raise SystemExit("bench.py: no GPU visible to libnship")
+    rows = workloads.CONFIGS["c2"].rows
+    plan = runtime.Plan.load("c2")
+    shapes = workloads.ir_shapes(plan.ir)
+    w = workloads.weights("c2", plan.layout(), shapes)
+    x = workloads.inputs("c2")
+    model = runtime.Model(plan, w)
+    dx = runtime.DeviceArray.from_host(x)
+    dy = runtime.DeviceArray(rows * 1024)
+    for _ in range(warmup):
+        model.eval_infer_device(dx, dy)
+    model.sync()
+    # timed region: K forward steps, per-launch HIP events on the model stream
+    model.profile(True)
+    model.profile_reset()
+    model.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.eval_infer_device(dx, dy)
+    model.sync()
+    dt = time.perf_counter() - t0
+    prof = model.profile_report()
+    model.profile(False)
+    out = dy.to_host()
+    if not np.isfinite(out).all():
+        raise SystemExit("bench.py: non-finite output")
+    # host-pointer ABI rate (PCIe-inclusive), for reference only
+    t0 = time.perf_counter()
+    for _ in range(3):
+        model.eval_infer(x)
+    abi_dt = (time.perf_counter() - t0) / 3
+
+    gemm_calls = sum(v["calls"] for k, v in prof.items() if k.startswith("gemm"))
+    gemm_ms = sum(v["ms"] for k, v in prof.items() if k.startswith("gemm"))
+    per_launch_ms = gemm_ms / max(gemm_calls, 1)
+    flop_per_launch = c2_flops(rows) / 3.0
+    achieved = flop_per_launch / (per_launch_ms * 1e-3) / 1e12
+    res = {
+        "metric": METRIC,
+        "value": rows * steps / dt,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": dt * 1e3 / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "c2: " + workloads.CONFIGS["c2"].desc, "batch": rows,
+                   "layers": "1024->4096->4096->1024", "entry": "nsh_eval_infer_device"},
+        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel", "achieved": achieved,
+                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_F32_PEAK_TFLOPS,
+                     "flop_per_launch": flop_per_launch, "avg_launch_ms": per_launch_ms,
+                     "launches": gemm_calls, "traffic": load_traffic("gemm_f32_kernel")},
+        "host_abi": {"tokens_per_s": rows / abi_dt, "note": "ns_eval_infer with host buffers (PCIe-inclusive)"},
+    }
+    model.free()
+    if with_cpu:
+        res["cpu_baseline"] = cpu_baseline_c2()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c2", choices=["c2"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        raise SystemExit("bench.py: this build measures one GPU only (single-GPU boxes; "
+                         "see DESIGN.md for how the path would shard)")
+    res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

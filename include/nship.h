@@ -1,0 +1,111 @@
+/*
+ * nship.h -- C-ABI of libnship, the MI355X (gfx950) HIP backend behind the
+ * NeuralScript runtime ABI.
+ *
+ * Three layers, all plain C types (no HIP or torch types in signatures):
+ *
+ *  1. Plans.  A network is described by the text the reference compiler
+ *     prints for `nsc <net>.ns --mlir` (printer:
+ *     /root/reference/src/mlir/mlir_compiler.cpp:949-1025).  It replaces the
+ *     code the reference generates per network (gen_cpu / gen_cuda,
+ *     /root/reference/src/codegen/codegen.cpp:306-1132, 1133-2657): instead
+ *     of emitting kernels, the backend interprets the instruction list with
+ *     fixed, hand-written gfx950 kernels.  Attributes the printer drops can be
+ *     added to an instruction's trailing comment as key=value
+ *     (`initial=K0` on ns.layer.moe for MoE(initial_experts: K0)).
+ *
+ *  2. Models.  nsh_model_* / nsh_* mirror the ns_* runtime functions one for
+ *     one (ns_runtime.h); a per-network library (see neuralscript_amd/emit.py)
+ *     binds one plan and exports the ns_* names as thin wrappers.
+ *     nsh_*_device variants take device pointers and enqueue on the model's
+ *     stream without host copies.
+ *
+ *  3. Kernels.  nsh_op_* run one hand-written kernel family on device
+ *     pointers (synchronously), for hosts that drive the kernels directly and
+ *     for per-kernel parity tests.  Each cites the reference function whose
+ *     arithmetic it reproduces.
+ *
+ * Errors: functions return 0 / -1 (NULL for constructors) like the reference;
+ * nsh_last_error() gives the calling thread's last message.
+ */
+#ifndef NSHIP_H
+#define NSHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ns_runtime.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct nsh_plan nsh_plan;
+
+/* ---- errors and device helpers ---------------------------------------- */
+const char* nsh_last_error(void);
+int nsh_device_count(void);
+/* Device memory for hosts (and tests) that do not own a HIP allocator. */
+void* nsh_dev_alloc(size_t bytes);
+int nsh_dev_free(void* p);
+int nsh_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int nsh_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int nsh_memset_d(void* dst, int value, size_t bytes);
+int nsh_device_synchronize(void);
+
+/* ---- plans (replace the per-network generated driver tables,
+ *      codegen.cpp:2438-2466 / 917-941) ------------------------------------ */
+nsh_plan* nsh_plan_parse(const char* ir_text);
+void nsh_plan_free(nsh_plan* p);
+size_t nsh_plan_weight_count(const nsh_plan* p);              /* ns_weight_total */
+const ns_weight_layout* nsh_plan_layout(const nsh_plan* p);   /* ns_layout */
+size_t nsh_plan_output_numel(const nsh_plan* p, size_t input_numel); /* codegen.cpp:2481-2483 */
+int nsh_plan_has_train(const nsh_plan* p);
+int nsh_plan_has_moe(const nsh_plan* p);
+size_t nsh_plan_in_cols(const nsh_plan* p);
+size_t nsh_plan_out_cols(const nsh_plan* p);
+
+/* ---- models: one per ns_* function ------------------------------------- */
+ns_model* nsh_model_init(const nsh_plan* p, const float* weights, size_t num_floats); /* codegen.cpp:2467-2474 */
+void nsh_model_free(ns_model* m);                                                    /* :2497-2499 */
+int nsh_eval_infer(ns_model* m, const float* input, float* output, size_t input_numel); /* :2475-2480 */
+size_t nsh_model_weight_count(const ns_model* m);
+int nsh_model_get_weights(const ns_model* m, float* out, size_t n);                  /* :2490-2494 */
+int nsh_save_checkpoint(const ns_model* m, const char* path);                        /* :2505-2528 */
+int nsh_load_checkpoint(ns_model* m, const char* path);                              /* :2529-2557 */
+size_t nsh_expert_count(const ns_model* m);                                          /* :2562-2565 */
+size_t nsh_expert_birth(ns_model* m, int n);                                         /* :2567-2595 */
+size_t nsh_expert_merge(ns_model* m, int a, int b);                                  /* :2597-2617 */
+size_t nsh_expert_kill(ns_model* m, int k);                                          /* :2619-2626 */
+int nsh_train_step(ns_model* m, const float* input, const float* labels,
+                   size_t input_numel, float* loss_out, float lr);                   /* :2636-2644 */
+int nsh_objective_loss(ns_model* m, const float* input, const float* labels,
+                       size_t input_numel, float* loss_out);                         /* :2645-2651 */
+
+/* Device-resident forward: input/output are device pointers; enqueued on the
+ * model's stream, returns before completion (nsh_model_sync waits). */
+int nsh_eval_infer_device(ns_model* m, const float* d_input, float* d_output, size_t input_numel);
+int nsh_model_sync(ns_model* m);
+
+/* Per-kernel timing with HIP events recorded on the model's stream around
+ * every launch.  The report is one JSON object: kernel -> {calls, ms}. */
+int nsh_profile_enable(ns_model* m, int on);
+int nsh_profile_reset(ns_model* m);
+int nsh_profile_report(ns_model* m, char* buf, size_t len);
+
+/* ---- kernels on device pointers (synchronous) --------------------------- */
+
+/* C[M,N] = opA(A) opB(B) then activation `act` (0 id, 1 relu, 2 leaky,
+ * 3 sigmoid, 4 tanh, 5 silu, 6 gelu).  opA(A)[m,k] = transA ? A[k*lda+m] :
+ * A[m*lda+k]; opB(B)[k,n] = transB ? B[n*ldb+k] : B[k*ldb+n].
+ * Replaces ns_matmul + ns_act2 (codegen.cpp:1257-1265, 1244-1255),
+ * ns_matmul_grad_a (transB, :1318-1326) and ns_matmul_grad_w (transA,
+ * :1329-1337); fp32 MFMA. */
+int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, int transA, int transB, int act);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSHIP_H */

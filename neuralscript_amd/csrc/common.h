@@ -1,0 +1,84 @@
+// Shared host/device helpers for libnship (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace nship {
+
+// Thread-local last error (read by nsh_last_error).
+void set_error(const std::string& msg);
+
+#define NSH_CHECK(expr)                                                          \
+  do {                                                                           \
+    hipError_t e_ = (expr);                                                      \
+    if (e_ != hipSuccess) {                                                      \
+      ::nship::set_error(std::string(#expr) + ": " + hipGetErrorString(e_));     \
+      return -1;                                                                 \
+    }                                                                            \
+  } while (0)
+
+// Check a kernel launch issued just before.
+#define NSH_LAUNCHED()                                                           \
+  do {                                                                           \
+    hipError_t e_ = hipGetLastError();                                           \
+    if (e_ != hipSuccess) {                                                      \
+      ::nship::set_error(std::string("kernel launch: ") + hipGetErrorString(e_)); \
+      return -1;                                                                 \
+    }                                                                            \
+  } while (0)
+
+constexpr int kWave = 64;
+
+// Activation codes shared with the reference's ns_act2 switch
+// (codegen.cpp:1244-1255): 0 id, 1 relu, 2 leaky, 3 sigmoid, 4 tanh,
+// 5 silu, 6 gelu.
+enum Act : int { kActId = 0, kActRelu, kActLeaky, kActSigmoid, kActTanh, kActSilu, kActGelu };
+
+__device__ __forceinline__ float act_apply(float x, int code) {
+  switch (code) {
+    case kActRelu: return x > 0.f ? x : 0.f;
+    case kActLeaky: return x > 0.f ? x : 0.01f * x;
+    case kActSigmoid: return 1.f / (1.f + expf(-x));
+    case kActTanh: return tanhf(x);
+    case kActSilu: return x / (1.f + expf(-x));
+    case kActGelu: return 0.5f * x * (1.f + erff(x / 1.41421356f));
+    default: return x;
+  }
+}
+
+// d act / dx at the pre-activation x (codegen.cpp:1305-1315).
+__device__ __forceinline__ float act_deriv(float x, int code) {
+  switch (code) {
+    case kActRelu: return x > 0.f ? 1.f : 0.f;
+    case kActLeaky: return x > 0.f ? 1.f : 0.01f;
+    case kActSigmoid: { float s = 1.f / (1.f + expf(-x)); return s * (1.f - s); }
+    case kActTanh: { float t = tanhf(x); return 1.f - t * t; }
+    case kActSilu: { float s = x / (1.f + expf(-x)); return s + x * (1.f - s); }
+    case kActGelu: {
+      float u = x / 1.41421356f;
+      float p = 0.5f * (1.f + erff(u));
+      return p + x * expf(-u * u) / 2.50662827f;
+    }
+    default: return 1.f;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace nship

@@ -1,0 +1,255 @@
+// fp32 MFMA GEMM for gfx950 (CDNA4):  C[M,N] = act( opA(A) . opB(B) ).
+//
+// Replaces the reference's dense products and their activation passes:
+//   ns_matmul + ns_act2          /root/reference/src/codegen/codegen.cpp:1257-1265, 1244-1255
+//   ns_matmul_grad_a  (transB)   codegen.cpp:1318-1326
+//   ns_matmul_grad_w  (transA)   codegen.cpp:1329-1337
+// (CUDA counterparts ns_gemm_kernel / ns_grad_a_kernel / ns_grad_w_kernel,
+// /root/reference/src/codegen/cuda_backend.cpp:58-79, 446-467.)
+//
+// Design (wave64, MFMA 32x32x2 fp32, true fp32 products and sums):
+//  * 256-thread workgroup = 4 waves in a 2x2 grid; workgroup tile 128x128,
+//    wave tile 64x64 = 2x2 MFMA blocks of 32x32 (64 accumulators per lane).
+//  * K advances in 16-wide slabs staged in LDS, double buffered: the next
+//    slab's global loads are in flight while the current slab feeds the
+//    MFMAs; one barrier per slab.
+//  * Each operand keeps its global memory order in LDS (no transposing
+//    stores): k-contiguous operands are read back as float4 along k,
+//    row-contiguous operands as four scalars.  Within a 16-slab, lane half h
+//    of MFMA step q of group g consumes k = 8g + 4h + q for BOTH operands, a
+//    fixed bijection, so the contraction is unchanged.
+//  * Workgroup ids are remapped so each XCD (ids are dealt round-robin over
+//    the 8 XCDs) owns a contiguous run of tiles, grouped 8 tile-rows at a
+//    time for L2 reuse of the B panel.
+//  * The activation is applied to the accumulators before the single store.
+#include "common.h"
+
+namespace nship {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int KPAD = 4;    // pitch of k-contiguous rows: 20 floats
+constexpr int RPAD = 4;    // pitch of row-contiguous k rows: 132 floats
+constexpr int NT = 256;
+
+// LDS floats for one operand tile in either layout.
+constexpr int KC_TILE = BM * (BK + KPAD);   // [128][20]
+constexpr int MC_TILE = BK * (BM + RPAD);   // [16][132]
+
+template <bool KC>
+struct TileLayout;
+template <>
+struct TileLayout<true> {  // [rows][k], k contiguous
+  static constexpr int kSize = KC_TILE;
+  __device__ static int at(int row, int k) { return row * (BK + KPAD) + k; }
+};
+template <>
+struct TileLayout<false> {  // [k][rows], rows contiguous
+  static constexpr int kSize = MC_TILE;
+  __device__ static int at(int row, int k) { return k * (BM + RPAD) + row; }
+};
+
+// Global -> register staging of one 128x16 operand tile.
+//  KC: element (row, k) at base[row*ld + k]   (k contiguous)
+//  MC: element (row, k) at base[k*ld + row]   (row contiguous)
+// `rows` = extent of the row dimension (M or N), `K` = contraction extent.
+template <bool KC, bool VEC>
+struct Stage {
+  float v[8];
+  __device__ void load(const float* __restrict__ base, int64_t ld, int row0, int rows, int k0, int K,
+                       int t) {
+    if (VEC) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int idx = t + NT * i;
+        int r, k;
+        if (KC) { r = idx >> 2; k = (idx & 3) * 4; } else { k = idx >> 5; r = (idx & 31) * 4; }
+        const int gr = row0 + r, gk = k0 + k;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        // Whole float4 in or out: the contiguous extent is a multiple of 4.
+        if (gr < rows && gk < K) {
+          const float* p = KC ? base + (int64_t)gr * ld + gk : base + (int64_t)gk * ld + gr;
+          x = *reinterpret_cast<const float4*>(p);
+        }
+        v[4 * i + 0] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int idx = t + NT * i;
+        int r, k;
+        if (KC) { r = idx >> 4; k = idx & 15; } else { k = idx >> 7; r = idx & 127; }
+        const int gr = row0 + r, gk = k0 + k;
+        float x = 0.f;
+        if (gr < rows && gk < K) x = KC ? base[(int64_t)gr * ld + gk] : base[(int64_t)gk * ld + gr];
+        v[i] = x;
+      }
+    }
+  }
+  __device__ void store(float* __restrict__ lds, int t) const {
+    if (VEC) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int idx = t + NT * i;
+        int r, k;
+        if (KC) { r = idx >> 2; k = (idx & 3) * 4; } else { k = idx >> 5; r = (idx & 31) * 4; }
+        float* p = lds + TileLayout<KC>::at(r, k);
+        *reinterpret_cast<float4*>(p) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int idx = t + NT * i;
+        int r, k;
+        if (KC) { r = idx >> 4; k = idx & 15; } else { k = idx >> 7; r = idx & 127; }
+        lds[TileLayout<KC>::at(r, k)] = v[i];
+      }
+    }
+  }
+};
+
+// Four operand values of one lane for MFMA steps q = 0..3 of group g.
+template <bool KC>
+__device__ __forceinline__ void read_frag(const float* __restrict__ lds, int row, int kb, float f[4]) {
+  if (KC) {
+    const float4 x = *reinterpret_cast<const float4*>(lds + TileLayout<true>::at(row, kb));
+    f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; q++) f[q] = lds[TileLayout<false>::at(row, kb + q)];
+  }
+}
+
+// Logical tile of workgroup b: XCD-contiguous runs, then 8-row groups.
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int T = tiles_m * tiles_n;
+  const int per = T >> 3, rem = T & 7;
+  const int x = b & 7, i = b >> 3;
+  const int L = x * per + (x < rem ? x : rem) + i;
+  const int group = 8 * tiles_n;
+  const int first_m = (L / group) * 8;
+  const int gsize = min(tiles_m - first_m, 8);
+  const int in = L % group;
+  tm = first_m + in % gsize;
+  tn = in / gsize;
+}
+
+// opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
+// opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
+template <bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ A,
+                                                      const float* __restrict__ B,
+                                                      float* __restrict__ C, int M, int N, int K,
+                                                      int64_t lda, int64_t ldb, int64_t ldc, int act,
+                                                      int tiles_m, int tiles_n) {
+  constexpr bool AKC = !TA, BKC = TB;
+  constexpr int ASZ = TileLayout<AKC>::kSize, BSZ = TileLayout<BKC>::kSize;
+  __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
+  // buffer b: A tile at smem + b*(ASZ+BSZ), B tile right after it
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, kh = lane >> 5;
+
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) acc[r][c][v] = 0.f;
+
+  Stage<AKC, VEC> sa;
+  Stage<BKC, VEC> sb;
+  const int nk = (K + BK - 1) / BK;
+  sa.load(A, lda, m0, M, 0, K, t);
+  sb.load(B, ldb, n0, N, 0, K, t);
+  sa.store(smem, t);
+  sb.store(smem + ASZ, t);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      sa.load(A, lda, m0, M, (kt + 1) * BK, K, t);
+      sb.load(B, ldb, n0, N, (kt + 1) * BK, K, t);
+    }
+    const float* as = smem + cur * (ASZ + BSZ);
+    const float* bs = as + ASZ;
+#pragma unroll
+    for (int g = 0; g < 2; g++) {
+      const int kb = 8 * g + 4 * kh;
+      float fa[2][4], fb[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; r++) read_frag<AKC>(as, wm * 64 + r * 32 + l32, kb, fa[r]);
+#pragma unroll
+      for (int c = 0; c < 2; c++) read_frag<BKC>(bs, wn * 64 + c * 32 + l32, kb, fb[c]);
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+          for (int c = 0; c < 2; c++)
+            acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[r][q], fb[c][q], acc[r][c], 0, 0, 0);
+    }
+    if (more) {
+      float* nxt = smem + (cur ^ 1) * (ASZ + BSZ);
+      sa.store(nxt, t);
+      sb.store(nxt + ASZ, t);
+    }
+    __syncthreads();
+  }
+
+  // Accumulator v of lane (l32, kh) in a 32x32 block sits at
+  // row 8*(v/4) + 4*kh + v%4, column l32.
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int col = n0 + wn * 64 + c * 32 + l32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = m0 + wm * 64 + r * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+        if (row < M) C[(int64_t)row * ldc + col] = act_apply(acc[r][c][v], act);
+      }
+    }
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Host launcher.  Returns 0 / -1.
+int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, bool tA, bool tB, int act, hipStream_t s) {
+  if (M <= 0 || N <= 0) return 0;
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+    set_error("gemm: dimension exceeds int32");
+    return -1;
+  }
+  // float4 staging needs each operand's contiguous extent, leading dimension
+  // and base to be 4-float aligned.
+  const bool va = aligned16(A) && (lda % 4 == 0) && ((tA ? M : K) % 4 == 0);
+  const bool vb = aligned16(B) && (ldb % 4 == 0) && ((tB ? K : N) % 4 == 0);
+  const bool vec = va && vb;
+  const int tiles_m = (int)ceil_div(M, BM), tiles_n = (int)ceil_div(N, BN);
+  const dim3 grid(tiles_m * tiles_n), block(NT);
+  const int m = (int)M, n = (int)N, k = (int)K;
+#define NSH_GEMM(TA_, TB_, V_) \
+  hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_>), grid, block, 0, s, A, B, C, m, n, k, lda, ldb, ldc, act, tiles_m, tiles_n)
+  if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
+  else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
+  else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
+  else { if (vec) NSH_GEMM(true, true, true); else NSH_GEMM(true, true, false); }
+#undef NSH_GEMM
+  NSH_LAUNCHED();
+  return 0;
+}
+
+}  // namespace nship

@@ -1,0 +1,71 @@
+// Network plan: the instruction list of `nsc --mlir` (printer at
+// /root/reference/src/mlir/mlir_compiler.cpp:949-1025), resolved into value
+// ids, weight offsets and per-op attributes.  Pure host code.
+#pragma once
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ns_runtime.h"
+
+namespace nship {
+
+enum class Op {
+  Alloc, Marker, Matmul, Act, Dropout, LayerNorm, Embedding, Attention, Moe, CrossEntropy,
+  LossGrad, MatmulGradA, MatmulGradW, ActGrad, LayerNormGrad, EmbeddingGradW,
+  AttnGradX, AttnGradWq, AttnGradWk, AttnGradWv, AttnGradWo,
+  MoeGradX, MoeGradWg, MoeGradWe1, MoeGradWe2, OptStep
+};
+
+struct Instr {
+  Op op = Op::Marker;
+  int res = -1;               // value id of the result (-1: none)
+  std::vector<int> in;        // operand value ids
+  int act = 0;                // Act / ActGrad: activation code; Matmul: fused epilogue
+  int64_t rt_cols = -1;       // column count from the printed result type
+  int heads = 1;              // Attention / AttnGrad*
+  bool fused_away = false;    // Act folded into the preceding Matmul
+};
+
+struct Value {
+  std::string name;
+  bool weight = false;
+  int64_t rows = -1, cols = -1;  // weights: static shape
+  size_t offset = 0;             // weights: float offset in the blob
+};
+
+struct Func {
+  std::string name;
+  std::vector<Instr> ins;
+  int ret = -1;
+  bool train = false;
+  int x = -1;  // runtime data input
+  int y = -1;  // labels (training)
+  std::vector<int64_t> width;  // propagated column count per value id (-1 unknown)
+};
+
+struct MoeInfo {
+  bool present = false;
+  int64_t D = 0, E = 0, H = 0, K0 = 0;
+  int g = -1, e1 = -1, e2 = -1;  // weight value ids
+};
+
+struct Plan {
+  std::vector<Value> vals;
+  std::map<std::string, int> index;
+  std::vector<int> weights;  // value ids in TENSOR_ALLOC order
+  Func fwd, trn;
+  bool has_train = false;
+  size_t total = 0;
+  int64_t in_cols = 1, out_cols = 1;
+  MoeInfo moe;
+  std::vector<std::string> wnames;
+  std::vector<ns_weight_desc> desc;
+  ns_weight_layout layout{0, nullptr};
+};
+
+// Parses the IR text.  On failure returns nullptr and sets *err.
+Plan* parse_plan(const char* text, std::string* err);
+
+}  // namespace nship

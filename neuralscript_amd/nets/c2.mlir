@@ -1,0 +1,12 @@
+// NeuralScript MLIR
+ns.func @MLP {
+  ns.tensor.alloc %fc1_w : Tensor[1024, 4096] float32 // allocate weight [1024, 4096]
+  ns.tensor.alloc %fc2_w : Tensor[4096, 4096] float32 // allocate weight [4096, 4096]
+  ns.tensor.alloc %fc3_w : Tensor[4096, 1024] float32 // allocate weight [4096, 1024]
+  ns.matmul %fc0 %x %fc1_w // x -> fc1
+  ns.activation.gelu %act1 %fc0 // GELU(fc0)
+  ns.matmul %fc2 %act1 %fc2_w // act1 -> fc2
+  ns.activation.gelu %act3 %fc2 // GELU(fc2)
+  ns.matmul %fc4 %act3 %fc3_w // act3 -> fc3
+  ns.return %fc4
+}

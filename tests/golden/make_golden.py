@@ -1,0 +1,89 @@
+"""Write the golden fixtures of tests/golden/*.npz from the REFERENCE itself.
+
+Each case runs a network driver emitted by the reference compiler
+(`nsc <net>.ns --cpp --runtime`, compiled by oracle/Makefile into
+oracle/_ref/lib<net>.so exactly as the reference tests compile it) through
+its C-ABI on seeded inputs, and stores what it returned: the forward output,
+and for training cases the per-step losses, the objective loss and the final
+weight blob.  Inputs are not stored; they are regenerated from the seeds
+(SplitMix64, neuralscript_amd/synth.py) and checked against a stored digest.
+
+Run in the build container (needs /root/reference built by oracle/Makefile):
+    python tests/golden/make_golden.py
+"""
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
+
+import helpers  # noqa: E402
+import oracle  # noqa: E402
+from neuralscript_amd.abi import NsLib  # noqa: E402
+
+XOR_X = np.array([0, 0, 0, 1, 1, 0, 1, 1], dtype=np.float32)
+XOR_Y = np.array([1, 0, 0, 1, 0, 1, 1, 0], dtype=np.float32)
+
+# name, rows, seed, train steps, lr, lifecycle
+CASES = [
+    ("c1", 64, 101, 0, 0.0, False),
+    ("c2s", 29, 102, 0, 0.0, False),
+    ("xor", 4, 103, 6, 0.3, False),
+    ("mlpt", 17, 104, 3, 0.01, False),
+    ("c3s", 45, 105, 0, 0.0, False),
+    ("c4s", 50, 106, 0, 0.0, False),
+    ("c4k", 40, 107, 0, 0.0, True),
+    ("c5t", 33, 108, 3, 0.01, False),
+    ("moet", 41, 109, 3, 0.01, False),
+    ("c5s", 64, 110, 2, 0.003, False),
+]
+
+
+def case_inputs(name, rows, seed):
+    net = oracle.Net(helpers.ir_text(name))
+    if name == "xor":
+        return net, XOR_X.copy(), XOR_Y.copy()
+    x = helpers.net_inputs(net, name, seed, rows)
+    y = helpers.net_labels(net, seed, rows) if net.train else None
+    return net, x, y
+
+
+def digest(a):
+    return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()[:16]
+
+
+def main():
+    for name, rows, seed, steps, lr, life in CASES:
+        net, x, y = case_inputs(name, rows, seed)
+        w = helpers.net_weights(name, seed)
+        lib = NsLib(os.path.join(helpers.REF, f"lib{name}.so"))
+        m = lib.init(w)
+        out = lib.eval_infer(m, x)[: net.output_numel(x.size) if net.moe is None else rows * net.moe["D"]]
+        rec = dict(out=out, x_digest=np.array(digest(x)), w_digest=np.array(digest(w)))
+        if steps:
+            rec["losses"] = np.array([lib.train_step(m, x, y, lr) for _ in range(steps)], dtype=np.float32)
+            rec["objective"] = np.float32(lib.objective_loss(m, x, y))
+            rec["w_final"] = lib.get_weights(m)
+            rec["out_after"] = lib.eval_infer(m, x)[: out.size]
+        if life:
+            outs, counts = [], []
+            counts.append(lib.lib.ns_expert_birth(m, 1))
+            outs.append(lib.eval_infer(m, x)[: out.size])
+            counts.append(lib.lib.ns_expert_merge(m, 0, 1))
+            outs.append(lib.eval_infer(m, x)[: out.size])
+            counts.append(lib.lib.ns_expert_kill(m, 2))
+            outs.append(lib.eval_infer(m, x)[: out.size])
+            rec["life_counts"] = np.array(counts, dtype=np.int64)
+            rec["life_outs"] = np.stack(outs)
+            rec["life_w"] = lib.get_weights(m)
+        lib.free(m)
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **rec)
+        print(name, {k: getattr(v, "shape", None) for k, v in rec.items()})
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,83 @@
+"""Whole networks through the ns_* C-ABI of the per-network drivers built on
+libnship, against the reference fixtures (tests/golden) and the oracle."""
+import os
+
+import numpy as np
+import pytest
+
+import helpers
+import oracle
+from golden.make_golden import CASES, case_inputs
+from neuralscript_amd import runtime, workloads
+
+pytestmark = pytest.mark.gpu
+
+FWD_NETS = ["c1", "c2s", "xor", "mlpt"]
+
+
+def golden(name):
+    return np.load(os.path.join(helpers.GOLDEN, f"{name}.npz"))
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[0] in FWD_NETS], ids=lambda c: c[0])
+def test_forward_matches_reference_fixture(case):
+    name, rows, seed = case[:3]
+    print(f"forward {name} rows={rows}", flush=True)
+    net, x, _ = case_inputs(name, rows, seed)
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, seed))
+    assert m
+    out = lib.eval_infer(m, x)
+    g = golden(name)["out"]
+    helpers.assert_close(out[: g.size], g, f"{name} forward")
+    lib.free(m)
+
+
+def test_c2_full_size_rows_match_oracle():
+    """Config 2 at its full batch (8192 x 1024 -> 4096 -> 4096 -> 1024, GELU);
+    the oracle recomputes 96 rows spread over the batch (rows are independent)."""
+    print("c2 full size", flush=True)
+    ir = helpers.ir_text("c2")
+    plan = runtime.Plan(ir)
+    shapes = workloads.ir_shapes(ir)
+    w = workloads.weights("c2", plan.layout(), shapes)
+    x = workloads.inputs("c2")
+    lib = runtime.net_lib("c2")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x).reshape(8192, 1024)
+    lib.free(m)
+    rows = np.unique(np.linspace(0, 8191, 96).astype(np.int64))
+    om = oracle.Model(oracle.Net(ir), w)
+    ref = om.eval_infer(x.reshape(8192, 1024)[rows]).reshape(len(rows), 1024)
+    helpers.assert_close(out[rows], ref, "c2 rows")
+    assert np.isfinite(out).all()
+
+
+def test_checkpoint_round_trip_and_errors(tmp_path):
+    name = "c2s"
+    lib = runtime.net_lib(name)
+    w0 = helpers.net_weights(name, 1)
+    w1 = helpers.net_weights(name, 2)
+    a, b = lib.init(w0), lib.init(w1)
+    pa, pb = str(tmp_path / "a.nsm"), str(tmp_path / "b.nsm")
+    assert lib.save(a, pa) == 0 and lib.save(b, pb) == 0
+    assert lib.load(a, pb) == 0
+    assert helpers.bitwise_equal(lib.get_weights(a), w1)
+    net = oracle.Net(helpers.ir_text(name))
+    x = helpers.net_inputs(net, name, 3, 11)
+    assert helpers.bitwise_equal(lib.eval_infer(a, x), lib.eval_infer(b, x))
+    assert lib.load(a, str(tmp_path / "missing.nsm")) == -1
+    assert lib.save(None, pa) == -1
+    with open(pa, "rb") as f:
+        raw = f.read()
+    assert raw[:4] == b"2MSN" and int.from_bytes(raw[4:12], "little") == w0.size
+    with open(str(tmp_path / "trunc.nsm"), "wb") as f:
+        f.write(raw[:100])
+    assert lib.load(a, str(tmp_path / "trunc.nsm")) == -1
+    assert helpers.bitwise_equal(lib.get_weights(a), w1)  # failed load leaves the model intact
+    assert lib.lib.ns_runtime_init(None, 0) is None
+    short = np.zeros(3, np.float32)
+    assert lib.init(short) is None
+    lib.free(a)
+    lib.free(b)
+    lib.free(None)

@@ -1,0 +1,263 @@
+"""The oracle is pinned before it is trusted:
+  * bit-for-bit against fixtures produced by the reference's own emitted
+    drivers (tests/golden, written by make_golden.py from oracle/_ref);
+  * bit-for-bit against the reference build on fresh seeds when that build is
+    present (this container);
+  * against closed forms that a plausible slip (dropped term, wrong index,
+    transposed operand) would break."""
+import os
+
+import numpy as np
+import pytest
+
+import helpers
+import oracle
+from neuralscript_amd import synth
+
+from golden.make_golden import CASES, case_inputs, digest
+
+pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
+
+
+def load_golden(name):
+    return np.load(os.path.join(helpers.GOLDEN, f"{name}.npz"))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_oracle_matches_reference_fixtures(case):
+    name, rows, seed, steps, lr, life = case
+    g = load_golden(name)
+    net, x, y = case_inputs(name, rows, seed)
+    w = helpers.net_weights(name, seed)
+    assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w_digest"]), "input generator drifted"
+    m = oracle.Model(net, w)
+    rec = {}
+    out = m.eval_infer(x, rec)
+    assert helpers.bitwise_equal(out, g["out"]), f"{name}: forward differs from the reference"
+    if steps:
+        losses = np.array([m.train_step(x, y, lr) for _ in range(steps)], dtype=np.float32)
+        assert helpers.bitwise_equal(losses, g["losses"]), f"{name}: losses {losses} vs {g['losses']}"
+        assert helpers.bitwise_equal(m.objective_loss(x, y), g["objective"])
+        assert helpers.bitwise_equal(m.w, g["w_final"]), f"{name}: trained weights differ"
+        assert helpers.bitwise_equal(m.eval_infer(x), g["out_after"])
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(helpers.REF, "libc5t.so")),
+                    reason="reference build (oracle/_ref) not present")
+@pytest.mark.parametrize("name,rows", [("c2s", 41), ("c3s", 70), ("c4k", 64), ("c5t", 50), ("moet", 23), ("mlpt", 9)])
+def test_oracle_matches_reference_build(name, rows):
+    from neuralscript_amd.abi import NsLib
+    net = oracle.Net(helpers.ir_text(name))
+    seed = 9000 + rows
+    x = helpers.net_inputs(net, name, seed, rows)
+    w = helpers.net_weights(name, seed, std=0.5)
+    lib = NsLib(os.path.join(helpers.REF, f"lib{name}.so"))
+    h = lib.init(w)
+    m = oracle.Model(net, w)
+    ref = lib.eval_infer(h, x)
+    out = m.eval_infer(x)
+    assert helpers.bitwise_equal(out, ref[: out.size])
+    if net.train:
+        y = helpers.net_labels(net, seed, rows)
+        for _ in range(2):
+            assert helpers.bitwise_equal(lib.train_step(h, x, y, 0.02), m.train_step(x, y, 0.02))
+        assert helpers.bitwise_equal(lib.get_weights(h), m.w)
+    lib.free(h)
+
+
+# ---- closed forms ---------------------------------------------------------
+
+def test_layernorm_rows_are_standardised():
+    x = synth.normal(1, 37 * 96, 3.0) + 5.0
+    y = oracle.layernorm(x, 96).reshape(37, 96).astype(np.float64)
+    var = x.reshape(37, 96).astype(np.float64).var(axis=1)
+    assert np.allclose(y.mean(axis=1), 0, atol=1e-5)
+    assert np.allclose(y.var(axis=1), var / (var + 1e-5), rtol=1e-4)
+
+
+def test_embedding_is_exact_row_copy_and_oor_maps_to_row0():
+    V, D = 11, 7
+    W = synth.normal(2, V * D)
+    idx = np.array([0, 3.9, 10, -0.5, -1, 11, 1e30, np.nan, -7], dtype=np.float32)
+    out = oracle.embedding(W, idx, V, D).reshape(-1, D)
+    expect_rows = [0, 3, 10, 0, 0, 0, 0, 0, 0]
+    assert np.array_equal(out, W.reshape(V, D)[expect_rows])
+    assert list(oracle.embedding_rows(idx, V)) == [0, 3, 10, 0, -1, -1, -1, -1, -1]
+
+
+def test_embedding_grad_is_scatter_add_skipping_oor():
+    V, D = 6, 5
+    idx = np.array([1, 4, 1, 9, -2, 1], dtype=np.float32)
+    d = synth.normal(3, idx.size * D).reshape(-1, D)
+    g = oracle.embedding_grad_w(d.ravel(), idx, V, D).reshape(V, D)
+    ref = np.zeros((V, D), np.float32)
+    ref[1] = (d[0] + d[2]) + d[5]
+    ref[4] = d[1]
+    assert np.array_equal(g, ref)
+
+
+def test_loss_grad_rows_sum_to_zero_and_ce_matches_log_softmax():
+    R, C = 9, 13
+    p = synth.normal(4, R * C, 2.0)
+    y = synth.one_hot(synth.token_ids(5, R, C), C)
+    g = oracle.loss_grad(p, y, C).reshape(R, C).astype(np.float64)
+    assert np.allclose(g.sum(axis=1), 0, atol=1e-7)
+    P = p.reshape(R, C).astype(np.float64)
+    ls = P - P.max(1, keepdims=True)
+    ls = ls - np.log(np.exp(ls).sum(1, keepdims=True))
+    ce = -(ls * y.reshape(R, C)).sum() / R
+    assert abs(oracle.cross_entropy(p, y, C) - ce) < 1e-5
+    sm = np.exp(ls)
+    assert np.allclose(g, (sm - y.reshape(R, C)) / R, atol=1e-7)
+
+
+def test_attention_with_identical_keys_averages_values():
+    # Wq = 0 makes every score equal, so each output row is mean(V) @ Wo.
+    BS, D, H = 10, 8, 2
+    x = synth.normal(6, BS * D)
+    Wq = np.zeros(D * D, np.float32)
+    Wk, Wv, Wo = (synth.normal(7 + i, D * D) for i in range(3))
+    out = oracle.attention_fwd(x, Wq, Wk, Wv, Wo, BS, D, H).reshape(BS, D)
+    V = x.reshape(BS, D).astype(np.float64) @ Wv.reshape(D, D)
+    ref = V.mean(0) @ Wo.reshape(D, D)
+    assert np.allclose(out, np.broadcast_to(ref, (BS, D)), atol=1e-5)
+
+
+def test_attention_forward_matches_float64_softmax_attention():
+    BS, D, H = 12, 16, 4
+    x = synth.normal(20, BS * D)
+    W = [synth.normal(21 + i, D * D, 0.3) for i in range(4)]
+    out = oracle.attention_fwd(x, *W, BS, D, H).reshape(BS, D)
+    X = x.reshape(BS, D).astype(np.float64)
+    Q, K, V = (X @ w.reshape(D, D) for w in W[:3])
+    ctx = np.zeros((BS, D))
+    dk = D // H
+    for h in range(H):
+        s = Q[:, h * dk:(h + 1) * dk] @ K[:, h * dk:(h + 1) * dk].T / np.sqrt(dk)
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        ctx[:, h * dk:(h + 1) * dk] = p @ V[:, h * dk:(h + 1) * dk]
+    assert np.allclose(out, ctx @ W[3].reshape(D, D), atol=2e-5)
+
+
+def _fd_check(f, args, idx, grad, eps=1e-3, tol=2e-2):
+    """Central finite difference (float64 loss) of f along argument idx."""
+    a = [np.array(v, dtype=np.float64) for v in args]
+    rng = np.random.default_rng(0)
+    for j in rng.choice(a[idx].size, size=min(6, a[idx].size), replace=False):
+        ap = [v.copy() for v in a]
+        am = [v.copy() for v in a]
+        ap[idx].flat[j] += eps
+        am[idx].flat[j] -= eps
+        fd = (f(*ap) - f(*am)) / (2 * eps)
+        assert abs(fd - grad.flat[j]) <= tol * max(1.0, abs(fd)), (j, fd, grad.flat[j])
+
+
+def test_attention_backward_matches_finite_differences():
+    BS, D, H = 6, 8, 2
+    x = synth.normal(30, BS * D, 0.5)
+    W = [synth.normal(31 + i, D * D, 0.4) for i in range(4)]
+    dout = synth.normal(40, BS * D)
+    grads = oracle.attention_bwd(dout, x, *W, BS, D, H)
+
+    def loss(x_, wq, wk, wv, wo):
+        o = oracle.attention_fwd(*(np.asarray(v, np.float32) for v in (x_, wq, wk, wv, wo)), BS, D, H)
+        return float(np.dot(o.astype(np.float64), dout))
+
+    for i, g in enumerate(grads):
+        _fd_check(loss, [x] + W, i, g)
+
+
+def test_moe_single_live_expert_has_unit_probability():
+    M, D, H, E = 7, 6, 5, 4
+    x = synth.normal(50, M * D)
+    Wg, We1, We2 = synth.normal(51, D * E), synth.normal(52, E * D * H), synth.normal(53, E * H * D)
+    act = np.array([0, 0, 1, 0], np.uint8)
+    out, best, prob = oracle.moe_fwd(x, Wg, We1, We2, act, M, D, H, E)
+    assert (best == 2).all() and (prob == 1.0).all()
+    X = x.reshape(M, D).astype(np.float64)
+    h = X @ We1.reshape(E, D, H)[2]
+    from math import erf
+    g = 0.5 * h * (1 + np.vectorize(erf)(h / np.sqrt(2)))
+    assert np.allclose(out.reshape(M, D), g @ We2.reshape(E, H, D)[2], atol=1e-5)
+
+
+def test_moe_backward_matches_finite_differences():
+    M, D, H, E = 5, 4, 6, 3
+    x = synth.normal(60, M * D)
+    Wg, We1, We2 = synth.normal(61, D * E), synth.normal(62, E * D * H, 0.5), synth.normal(63, E * H * D, 0.5)
+    dout = synth.normal(64, M * D)
+    grads = oracle.moe_bwd(dout, x, Wg, We1, We2, None, M, D, H, E)
+
+    def loss(x_, g_, e1, e2):
+        o, _, _ = oracle.moe_fwd(*(np.asarray(v, np.float32) for v in (x_, g_, e1, e2)), None, M, D, H, E)
+        return float(np.dot(o.astype(np.float64), dout))
+
+    for i, g in enumerate(grads):
+        _fd_check(loss, [x, Wg, We1, We2], i, g, eps=1e-3, tol=3e-2)
+
+
+def test_matmul_grads_are_transposed_products():
+    M, K, N = 9, 7, 5
+    A, B, dC = synth.normal(70, M * K), synth.normal(71, K * N), synth.normal(72, M * N)
+    dA = oracle.matmul_grad_a(dC, B, M, K, N).reshape(M, K)
+    dB = oracle.matmul_grad_w(A, dC, M, K, N).reshape(K, N)
+    assert np.allclose(dA, dC.reshape(M, N).astype(np.float64) @ B.reshape(K, N).T, atol=1e-5)
+    assert np.allclose(dB, A.reshape(M, K).astype(np.float64).T @ dC.reshape(M, N), atol=1e-5)
+
+
+def test_layernorm_grad_matches_finite_differences_at_unit_scale():
+    # The reference's LAYERNORM_GRAD (codegen.cpp:1346-1371) projects with
+    # (x - mean) * mean((x - mean) * d) and leaves out the 1/(var + eps)
+    # factor the true gradient has on that term, so it equals the true
+    # gradient exactly when var + eps = 1.  Rows are scaled to that variance;
+    # the bitwise fixture pins (c5t, c5s training) cover general rows.
+    R, C = 3, 10
+    z = synth.normal(80, R * C).reshape(R, C).astype(np.float64)
+    z = (z - z.mean(1, keepdims=True)) / z.std(1, keepdims=True)
+    x = (z * np.sqrt(1.0 - 1e-5)).astype(np.float32).ravel()
+    d = synth.normal(81, R * C)
+    g = oracle.layernorm_grad(d, x, C)
+    _fd_check(lambda x_: float(np.dot(oracle.layernorm(np.asarray(x_, np.float32), C).astype(np.float64), d)),
+              [x], 0, g, eps=1e-2, tol=2e-2)
+
+
+def test_layernorm_grad_projection_term_lacks_inverse_variance():
+    # Away from unit variance the reference formula differs from the true
+    # gradient by exactly the (1 - inv^2) share of the projection term.
+    R, C = 2, 12
+    x = synth.normal(82, R * C, 3.0)
+    d = synth.normal(83, R * C)
+    g = oracle.layernorm_grad(d, x, C).reshape(R, C).astype(np.float64)
+    X, Dd = x.reshape(R, C).astype(np.float64), d.reshape(R, C).astype(np.float64)
+    xc = X - X.mean(1, keepdims=True)
+    inv = 1.0 / np.sqrt((xc ** 2).mean(1, keepdims=True) + 1e-5)
+    gamma = (xc * Dd).mean(1, keepdims=True)
+    true = inv * (Dd - Dd.mean(1, keepdims=True) - xc * inv ** 2 * gamma)
+    assert np.allclose(g - true, -inv * xc * gamma * (1 - inv ** 2), atol=1e-5)
+
+
+@pytest.mark.parametrize("r,c", [(40, 12), (12, 40), (16, 16)])
+def test_mgs_gives_orthonormal_q_with_positive_r(r, c):
+    G = synth.normal(90 + r, r * c)
+    Q = oracle.orthonom(G, r, c).reshape(r, c).astype(np.float64)
+    G2 = G.reshape(r, c).astype(np.float64)
+    if r < c:
+        Q, G2 = Q.T, G2.T
+    assert np.allclose(Q.T @ Q, np.eye(Q.shape[1]), atol=1e-4)
+    R = Q.T @ G2
+    assert np.allclose(np.tril(R, -1), 0, atol=1e-4) and (np.diag(R) > 0).all()
+
+
+def test_lr_cosine_schedule_values():
+    # warmup ramp from 0, then a half cosine to 0.05 (optim_params.hpp:54-62)
+    assert oracle.lr_scale_cosine(0) == 0.0
+    assert oracle.lr_scale_cosine(50) == np.float32(0.5)
+    assert abs(oracle.lr_scale_cosine(100) - 1.0) < 1e-6
+    assert abs(oracle.lr_scale_cosine(10000) - 0.05) < 1e-6
+    assert abs(oracle.lr_scale_cosine(5050) - (0.05 + 0.475)) < 1e-3
+
+
+def test_optimizer_rule_by_shape():
+    assert oracle.use_muon(8, 8) and oracle.use_muon(512, 8192)
+    assert not oracle.use_muon(7, 100) and not oracle.use_muon(1, 64) and not oracle.use_muon(2, 16)
