@@ -81,6 +81,61 @@ def cpu_baseline_c2(budget_s=12.0):
                       f"{dt:.1f} s, single-threaded as the reference emits it"}
 
 
+# Algorithmic work per forward of the other configs (FLOP, and bytes of the
+# bandwidth-bound kernels), for the per-kernel breakdown of --config runs.
+def c3_work(M=16384, D=1024, H=16, V=32000):
+    # gemm: 4 projections; attention: QK^T + PV over all heads;
+    # embedding / layernorm: bytes (one read + one write of [M, D] fp32)
+    return {"gemm": 2.0 * M * D * D * 4, "attention_fwd": 4.0 * M * M * D,
+            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4}
+
+
+def c4_work(M=65536, D=1024, E=64, H=1024):
+    return {"moe": 2.0 * M * D * E + 4.0 * M * D * H}
+
+
+def bench_forward(key, steps, warmup):
+    """Device-resident forward of config `key`; per-kernel HIP-event times."""
+    from neuralscript_amd import runtime, workloads
+    if not runtime.has_gpu():
+        raise SystemExit("bench.py: no GPU visible to libnship")
+    wl = workloads.CONFIGS[key]
+    plan = runtime.Plan.load(wl.net)
+    w = workloads.weights(key, plan.layout(), workloads.ir_shapes(plan.ir))
+    x = workloads.inputs(key)
+    model = runtime.Model(plan, w)
+    dx = runtime.DeviceArray.from_host(x)
+    dy = runtime.DeviceArray(wl.rows * plan.out_cols)
+    for _ in range(warmup):
+        model.eval_infer_device(dx, dy)
+    model.sync()
+    model.profile(True)
+    model.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.eval_infer_device(dx, dy)
+    model.sync()
+    dt = time.perf_counter() - t0
+    prof = model.profile_report()
+    model.free()
+    work = {"c3": c3_work, "c4": c4_work}.get(key, lambda: {})()
+    kernels = {}
+    for k, v in prof.items():
+        ms = v["ms"] / steps
+        e = {"ms_per_step": ms, "calls_per_step": v["calls"] / steps}
+        if k in work:
+            if k in ("embedding", "layernorm"):  # work = bytes read + written
+                e["GB/s"] = work[k] / (ms * 1e-3) / 1e9
+            else:
+                e["TFLOP/s"] = work[k] / (ms * 1e-3) / 1e12
+        kernels[k] = e
+    return {"metric": METRIC, "value": wl.rows * steps / dt, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device"},
+            "kernels": kernels}
+
+
 def bench_c2(steps, warmup, with_cpu):
     from neuralscript_amd import runtime, workloads
     if not runtime.has_gpu():
@@ -154,13 +209,17 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c2"])
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4"],
+                    help="c2 (default) is the metric's workload; c3/c4 print per-kernel breakdowns")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
         raise SystemExit("bench.py: this build measures one GPU only (single-GPU boxes; "
                          "see DESIGN.md for how the path would shard)")
-    res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
+    if a.config == "c2":
+        res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
+    else:
+        res = bench_forward(a.config, a.steps, a.warmup)
     print(json.dumps(res), flush=True)
 
 

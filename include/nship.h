@@ -87,6 +87,11 @@ int nsh_objective_loss(ns_model* m, const float* input, const float* labels,
 int nsh_eval_infer_device(ns_model* m, const float* d_input, float* d_output, size_t input_numel);
 int nsh_model_sync(ns_model* m);
 
+/* Routing of the most recent MoE forward of n tokens: chosen expert (-1 if
+ * none live), its probability, and the raw router logits [n, E].  Any output
+ * may be NULL. */
+int nsh_model_last_routing(ns_model* m, int32_t* best, float* prob, float* logits, size_t n);
+
 /* Per-kernel timing with HIP events recorded on the model's stream around
  * every launch.  The report is one JSON object: kernel -> {calls, ms}. */
 int nsh_profile_enable(ns_model* m, int on);
@@ -103,6 +108,41 @@ int nsh_profile_report(ns_model* m, char* buf, size_t len);
  * :1329-1337); fp32 MFMA. */
 int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, int transA, int transB, int act);
+
+/* out[i,:] = W[row(idx[i]),:], out-of-range or non-integral-range ids -> row 0;
+ * ns_embedding, codegen.cpp:1711-1718. */
+int nsh_op_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D);
+
+/* Row LayerNorm, no affine, eps 1e-5; ns_layernorm, codegen.cpp:1280-1291. */
+int nsh_op_layernorm(const float* x, float* y, int64_t rows, int64_t last);
+
+/* The reference's LayerNorm gradient; ns_layernorm_grad, codegen.cpp:1346-1371. */
+int nsh_op_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last);
+
+/* Softmax cross-entropy over rows of C: row_loss[r] = -sum_{y>0} log p,
+ * *loss = mean over rows, grad = (p - y) / rows (skipped when grad is NULL);
+ * ns_cross_entropy / ns_loss_grad, codegen.cpp:1582-1613.  loss and
+ * row_loss are device pointers. */
+int nsh_op_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
+                        int64_t rows, int64_t C);
+
+/* dout = din * act'(pre); ns_act_grad, codegen.cpp:1340-1343. */
+int nsh_op_act_grad(const float* din, const float* pre, float* dout, int64_t n, int act);
+
+/* dW[V,D] = scatter-add of dout rows by index, in token order (bit-exact
+ * with the reference's sequential loop); ns_embedding_grad_w,
+ * codegen.cpp:1374-1383.  `workspace`: device bytes from
+ * nsh_op_embedding_grad_workspace. */
+size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V);
+int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                          void* workspace);
+
+/* Attention core over one sequence of S tokens: ctx[S,D] = per-head
+ * softmax(Q K^T / sqrt(D/H)) V; Q, K, V are [S, D]; lse (optional, [H, S])
+ * receives each query's log2-sum-exp of the log2e-scaled scores; the core
+ * of ns_attention_fwd, codegen.cpp:1724-1777. */
+int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
+                         int64_t D, int64_t H);
 
 #ifdef __cplusplus
 }

@@ -23,6 +23,7 @@
 //    time for L2 reuse of the B panel.
 //  * The activation is applied to the accumulators before the single store.
 #include "common.h"
+#include "kernels.h"
 
 namespace nship {
 
@@ -57,8 +58,9 @@ struct TileLayout<false> {  // [k][rows], rows contiguous
 template <bool KC, bool VEC>
 struct Stage {
   float v[8];
+  // rmap (optional): row r of the operand is row rmap[r] of `base`.
   __device__ void load(const float* __restrict__ base, int64_t ld, int row0, int rows, int k0, int K,
-                       int t) {
+                       int t, const int* __restrict__ rmap = nullptr) {
     if (VEC) {
 #pragma unroll
       for (int i = 0; i < 2; i++) {
@@ -69,7 +71,8 @@ struct Stage {
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         // Whole float4 in or out: the contiguous extent is a multiple of 4.
         if (gr < rows && gk < K) {
-          const float* p = KC ? base + (int64_t)gr * ld + gk : base + (int64_t)gk * ld + gr;
+          const int64_t rr = rmap ? (int64_t)rmap[gr] : (int64_t)gr;
+          const float* p = KC ? base + rr * ld + gk : base + (int64_t)gk * ld + gr;
           x = *reinterpret_cast<const float4*>(p);
         }
         v[4 * i + 0] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
@@ -82,7 +85,10 @@ struct Stage {
         if (KC) { r = idx >> 4; k = idx & 15; } else { k = idx >> 7; r = idx & 127; }
         const int gr = row0 + r, gk = k0 + k;
         float x = 0.f;
-        if (gr < rows && gk < K) x = KC ? base[(int64_t)gr * ld + gk] : base[(int64_t)gk * ld + gr];
+        if (gr < rows && gk < K) {
+          const int64_t rr = rmap ? (int64_t)rmap[gr] : (int64_t)gr;
+          x = KC ? base[rr * ld + gk] : base[(int64_t)gk * ld + gr];
+        }
         v[i] = x;
       }
     }
@@ -138,11 +144,14 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
 template <bool TA, bool TB, bool VEC>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ A,
-                                                      const float* __restrict__ B,
-                                                      float* __restrict__ C, int M, int N, int K,
-                                                      int64_t lda, int64_t ldb, int64_t ldc, int act,
-                                                      int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
+  const int M = g.M, N = g.N, K = g.K;
+  const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
+  const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
+  const float* __restrict__ A = g.A + (int64_t)blockIdx.y * g.sA;
+  const float* __restrict__ B = g.B + (int64_t)blockIdx.y * g.sB;
+  float* __restrict__ C = g.C + (int64_t)blockIdx.y * g.sC;
+  int m_end = M;
   constexpr bool AKC = !TA, BKC = TB;
   constexpr int ASZ = TileLayout<AKC>::kSize, BSZ = TileLayout<BKC>::kSize;
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
@@ -153,9 +162,23 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ 
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, kh = lane >> 5;
 
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  int m0, n0;
+  if (g.groups) {
+    // Grouped: tile entry -> (group, m tile); rows [seg[e], seg[e+1]) of the
+    // group, B advanced by e * sBg.  Surplus workgroups exit (uniformly).
+    const int entry = blockIdx.x / tiles_n;
+    if (entry >= *g.ntiles) return;
+    const int e = g.tiles[2 * entry], mt = g.tiles[2 * entry + 1];
+    m0 = g.seg[e] + mt * BM;
+    m_end = g.seg[e + 1];
+    n0 = (blockIdx.x % tiles_n) * BN;
+    B += (int64_t)e * g.sBg;
+  } else {
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    m0 = tm * BM;
+    n0 = tn * BN;
+  }
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -168,7 +191,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ 
   Stage<AKC, VEC> sa;
   Stage<BKC, VEC> sb;
   const int nk = (K + BK - 1) / BK;
-  sa.load(A, lda, m0, M, 0, K, t);
+  sa.load(A, lda, m0, m_end, 0, K, t, g.a_rows);
   sb.load(B, ldb, n0, N, 0, K, t);
   sa.store(smem, t);
   sb.store(smem + ASZ, t);
@@ -178,7 +201,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ 
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      sa.load(A, lda, m0, M, (kt + 1) * BK, K, t);
+      sa.load(A, lda, m0, m_end, (kt + 1) * BK, K, t, g.a_rows);
       sb.load(B, ldb, n0, N, (kt + 1) * BK, K, t);
     }
     const float* as = smem + cur * (ASZ + BSZ);
@@ -218,31 +241,33 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const float* __restrict__ 
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int row = m0 + wm * 64 + r * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        if (row < M) C[(int64_t)row * ldc + col] = act_apply(acc[r][c][v], act);
+        if (row >= m_end) continue;
+        const int64_t crow = g.c_rows ? (int64_t)g.c_rows[row] : (int64_t)row;
+        float* dst = C + crow * ldc + col;
+        const float a = g.row_scale ? acc[r][c][v] * g.row_scale[crow] : acc[r][c][v];
+        if (g.mode == kEpiAct) *dst = act_apply(a, g.act);
+        else if (g.mode == kEpiActGrad) *dst = a * act_deriv(g.aux[(int64_t)row * g.ldaux + col], g.act);
+        else *dst = *dst + a;
       }
     }
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Host launcher.  Returns 0 / -1.
-int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
-                int64_t lda, int64_t ldb, int64_t ldc, bool tA, bool tB, int act, hipStream_t s) {
-  if (M <= 0 || N <= 0) return 0;
-  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
-    set_error("gemm: dimension exceeds int32");
-    return -1;
-  }
-  // float4 staging needs each operand's contiguous extent, leading dimension
-  // and base to be 4-float aligned.
-  const bool va = aligned16(A) && (lda % 4 == 0) && ((tA ? M : K) % 4 == 0);
-  const bool vb = aligned16(B) && (ldb % 4 == 0) && ((tB ? K : N) % 4 == 0);
+int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t s) {
+  if (in.M <= 0 || in.N <= 0 || batch <= 0) return 0;
+  GemmArgs g = in;
+  // float4 staging needs each operand's contiguous extent, leading dimension,
+  // batch stride and base to be 4-float aligned.
+  const bool va = aligned16(g.A) && g.lda % 4 == 0 && g.sA % 4 == 0 && ((tA ? g.M : g.K) % 4 == 0);
+  const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0);
   const bool vec = va && vb;
-  const int tiles_m = (int)ceil_div(M, BM), tiles_n = (int)ceil_div(N, BN);
-  const dim3 grid(tiles_m * tiles_n), block(NT);
-  const int m = (int)M, n = (int)N, k = (int)K;
-#define NSH_GEMM(TA_, TB_, V_) \
-  hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_>), grid, block, 0, s, A, B, C, m, n, k, lda, ldb, ldc, act, tiles_m, tiles_n)
+  g.tiles_m = (int)ceil_div(g.M, BM);
+  g.tiles_n = (int)ceil_div(g.N, BN);
+  // grouped: an upper bound on tile entries, sum_e ceil(n_e / BM) <= M/BM + E
+  const int entries = g.groups ? g.tiles_m + g.groups : g.tiles_m;
+  const dim3 grid(entries * g.tiles_n, batch), block(NT);
+#define NSH_GEMM(TA_, TB_, V_) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_>), grid, block, 0, s, g)
   if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
   else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
   else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
@@ -250,6 +275,20 @@ int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, 
 #undef NSH_GEMM
   NSH_LAUNCHED();
   return 0;
+}
+
+int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                int64_t lda, int64_t ldb, int64_t ldc, bool tA, bool tB, int act, hipStream_t s) {
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+    set_error("gemm: dimension exceeds int32");
+    return -1;
+  }
+  GemmArgs g;
+  g.A = A; g.B = B; g.C = C;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+  g.act = act;
+  return launch_gemm_ex(g, tA, tB, 1, s);
 }
 
 }  // namespace nship

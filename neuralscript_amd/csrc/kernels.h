@@ -7,8 +7,79 @@
 
 namespace nship {
 
-// gemm.hip
+// gemm.hip -------------------------------------------------------------------
+enum GemmEpilogue : int {
+  kEpiAct = 0,      // C = act(acc)
+  kEpiActGrad = 1,  // C = acc * act'(aux)      (matmul_grad_a fused with ACTIVATION_GRAD)
+  kEpiAccum = 2,    // C = C + acc
+};
+
+struct GemmArgs {
+  const float* A = nullptr;
+  const float* B = nullptr;
+  float* C = nullptr;
+  int M = 0, N = 0, K = 0;
+  int64_t lda = 0, ldb = 0, ldc = 0;
+  int64_t sA = 0, sB = 0, sC = 0;  // batch strides (blockIdx.y)
+  int act = 0;
+  int mode = kEpiAct;
+  const float* aux = nullptr;
+  int64_t ldaux = 0;
+  // Row gather / scatter (!transA only): operand-A row r is A row a_rows[r];
+  // output row r goes to C row c_rows[r], scaled by row_scale[c_rows[r]].
+  const int* a_rows = nullptr;
+  const int* c_rows = nullptr;
+  const float* row_scale = nullptr;
+  // Grouped mode (groups > 0): rows [seg[e], seg[e+1]) form group e and use
+  // B + e * sBg; `tiles` lists (group, m-tile) pairs, *ntiles of them.
+  int groups = 0;
+  const int* seg = nullptr;
+  const int* tiles = nullptr;
+  const int* ntiles = nullptr;
+  int64_t sBg = 0;
+  int tiles_m = 0, tiles_n = 0;    // filled by the launcher
+};
+
+int launch_gemm_ex(const GemmArgs& g, bool tA, bool tB, int batch, hipStream_t s);
 int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, bool tA, bool tB, int act, hipStream_t s);
+
+
+// rowops.hip -----------------------------------------------------------------
+int launch_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D, hipStream_t s);
+int launch_layernorm(const float* x, float* y, int64_t rows, int64_t last, hipStream_t s);
+int launch_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last, hipStream_t s);
+int launch_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
+                        int64_t rows, int64_t C, bool write_grad, hipStream_t s);
+int launch_act_grad(const float* din, const float* pre, float* dout, int64_t n, int code, hipStream_t s);
+size_t embedding_grad_workspace(int64_t n, int64_t V);  // ints
+int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D, int* ws,
+                          hipStream_t s);
+
+// attention.hip ----------------------------------------------------------------
+// ctx[S, D] (heads concatenated) = softmax(Q_h K_h^T * scale) V_h per head,
+// Q/K/V row-major [S, D] with row pitch ld.  lse (optional, [H, S]) receives
+// log2(sum_j 2^(s_j * scale * log2 e)) per query, for the backward pass.
+int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,
+                         int64_t H, int64_t ld, hipStream_t s);
+
+// moe.hip ----------------------------------------------------------------------
+struct MoeWork {
+  float* logits;   // [M, E]  raw router logits (kept for tie reports)
+  int* best;       // [M]     chosen expert, -1 if none live
+  float* prob;     // [M]     routing probability of the chosen expert
+  int* rank;       // [M]     rank of the token among same-expert tokens of its block
+  int* bcount;     // [nblk, E]
+  int* seg;        // [E + 1] segment starts of the expert-sorted order
+  int* perm;       // [M]     expert-sorted position -> token
+  int* tiles;      // [2 * (M/128 + E)] (expert, m-tile) pairs
+  int* ntiles;     // [1]
+  float* hidden;   // [M, H]  GELU(x We1[e]) in expert-sorted order
+};
+size_t moe_work_ints(int64_t M, int64_t E);   // int-sized words of all int arrays
+int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
+                     int64_t E, hipStream_t s);
+int launch_moe_experts(const float* x, const float* We1, const float* We2, const MoeWork& w, float* out, int64_t M,
+                       int64_t D, int64_t H, int64_t E, hipStream_t s);
 
 }  // namespace nship

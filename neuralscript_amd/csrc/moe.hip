@@ -1,0 +1,243 @@
+// Top-1 mixture of experts forward: router, dispatch, grouped expert GEMMs.
+//
+//   reference arithmetic: ns_moe_fwd, codegen.cpp:1915-1945
+//     lg_e = sum_k x_k Wg[k,e]    (one fp32 accumulator, k ascending, no FMA)
+//     mx = max over live e; lg_e = expf(lg_e - mx); sum over live e (ascending)
+//     best = first live e with a strictly larger exp'd value; p = lg_best / sum
+//     out = p * ( GELU(x We1[best]) We2[best] ),  GELU = 0.5 a (1 + erf(a/sqrt2))
+//
+// gfx950 design:
+//  * Router: the expert choice is an integer decision, so it must be
+//    bit-exact.  The logits are computed exactly as the reference does them
+//    (sequential k, separate multiply and add: contraction is switched off in
+//    this kernel), and exp is evaluated in double precision and rounded once
+//    to float, i.e. correctly rounded, which glibc's expf also is except
+//    within ~0.002 ulp of a rounding boundary.  x and Wg slabs are staged in
+//    LDS; each thread owns 16 tokens x E/64 experts.
+//  * Dispatch: per 256-token block, each token's rank among the block's
+//    tokens of the same expert and the block's per-expert counts; one scan
+//    turns those into expert segments and a STABLE permutation (tokens stay
+//    in order within their expert), plus the (expert, m-tile) list of the
+//    grouped GEMM -- all on the device, no host round trip.
+//  * Experts: two grouped fp32-MFMA GEMMs over the expert-sorted rows: the
+//    first gathers x rows through the permutation and applies GELU in its
+//    epilogue, the second scatters rows back to token order scaled by p.
+#include "common.h"
+#include "kernels.h"
+
+namespace nship {
+namespace {
+
+constexpr int kTok = 64;   // tokens per router workgroup
+constexpr int kKS = 32;    // k slab
+constexpr int kBlk = 256;  // tokens per dispatch block
+
+// exp(x) correctly rounded to float (double evaluation, one rounding).
+__device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
+
+template <int EPT>  // experts per thread / 64 (E <= 64 * EPT)
+__global__ __launch_bounds__(256) void moe_router_kernel(const float* __restrict__ x, const float* __restrict__ Wg,
+                                                         const uint8_t* __restrict__ active, float* __restrict__ logits,
+                                                         int* __restrict__ best, float* __restrict__ prob, int M,
+                                                         int D, int E) {
+#pragma clang fp contract(off)
+  __shared__ float xs[kTok][kKS + 1];
+  __shared__ float ws[kKS][64 * EPT];
+  __shared__ float lg[kTok][64 * EPT + 1];
+  const int t = threadIdx.x;
+  const int e0 = t & 63, tg = t >> 6;  // expert lane, token group (16 tokens)
+  const int tok0 = blockIdx.x * kTok;
+  float acc[16][EPT];
+#pragma unroll
+  for (int i = 0; i < 16; i++)
+#pragma unroll
+    for (int j = 0; j < EPT; j++) acc[i][j] = 0.f;
+
+  for (int k0 = 0; k0 < D; k0 += kKS) {
+    for (int i = t; i < kTok * kKS; i += 256) {
+      const int r = i / kKS, c = i % kKS;
+      const int tok = tok0 + r, k = k0 + c;
+      xs[r][c] = (tok < M && k < D) ? x[(int64_t)tok * D + k] : 0.f;
+    }
+    for (int i = t; i < kKS * 64 * EPT; i += 256) {
+      const int r = i / (64 * EPT), c = i % (64 * EPT);
+      const int k = k0 + r;
+      ws[r][c] = (k < D && c < E) ? Wg[(int64_t)k * E + c] : 0.f;
+    }
+    __syncthreads();
+    const int kn = min(kKS, D - k0);
+    for (int kk = 0; kk < kn; kk++) {
+#pragma unroll
+      for (int j = 0; j < EPT; j++) {
+        const float w = ws[kk][e0 + 64 * j];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const float prod = xs[tg * 16 + i][kk] * w;
+          acc[i][j] = acc[i][j] + prod;
+        }
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++)
+#pragma unroll
+    for (int j = 0; j < EPT; j++) lg[tg * 16 + i][e0 + 64 * j] = acc[i][j];
+  __syncthreads();
+
+  // Routing: one thread per token, experts in ascending order.
+  if (t < kTok && tok0 + t < M) {
+    const int tok = tok0 + t;
+    float* l = lg[t];
+    if (logits)
+      for (int e = 0; e < E; e++) logits[(int64_t)tok * E + e] = l[e];
+    float mx = -1.0e30f, sum = 0.f;
+    for (int e = 0; e < E; e++)
+      if ((!active || active[e]) && l[e] > mx) mx = l[e];
+    int b = -1;
+    for (int e = 0; e < E; e++) {
+      if (active && !active[e]) continue;
+      l[e] = exp_rn(l[e] - mx);
+      sum = sum + l[e];
+      if (b < 0 || l[e] > l[b]) b = e;
+    }
+    best[tok] = b;
+    prob[tok] = (sum > 0.f && b >= 0) ? l[b] / sum : 0.f;
+  }
+}
+
+// In-block rank of each token among same-expert tokens, and block counts.
+__global__ __launch_bounds__(kBlk) void moe_rank_kernel(const int* __restrict__ best, int* __restrict__ rank,
+                                                        int* __restrict__ bcount, int M, int E) {
+  __shared__ int b[kBlk];
+  const int t = threadIdx.x, tok = blockIdx.x * kBlk + t;
+  b[t] = tok < M ? best[tok] : -1;
+  __syncthreads();
+  const int mine = b[t];
+  int r = 0;
+  for (int j = 0; j < t; j++) r += b[j] == mine;
+  if (tok < M) rank[tok] = r;
+  for (int e = t; e < E; e += kBlk) {
+    int c = 0;
+    for (int j = 0; j < kBlk; j++) c += b[j] == e;
+    bcount[(int64_t)blockIdx.x * E + e] = c;
+  }
+}
+
+// Expert segments, per-block offsets (in place over bcount) and the
+// (expert, m-tile) list.  One workgroup; thread e owns expert e.
+__global__ __launch_bounds__(256) void moe_scan_kernel(int* __restrict__ bcount, int* __restrict__ seg,
+                                                       int* __restrict__ tiles, int* __restrict__ ntiles, int nblk,
+                                                       int E, int bm) {
+  __shared__ int tot[256], base[257], tb[257];
+  const int t = threadIdx.x;
+  for (int e = t; e < E; e += 256) {
+    int c = 0;
+    for (int k = 0; k < nblk; k++) c += bcount[(int64_t)k * E + e];
+    tot[e] = c;
+  }
+  __syncthreads();
+  if (t == 0) {
+    base[0] = 0;
+    tb[0] = 0;
+    for (int e = 0; e < E; e++) {
+      base[e + 1] = base[e] + tot[e];
+      tb[e + 1] = tb[e] + (tot[e] + bm - 1) / bm;
+    }
+    *ntiles = tb[E];
+  }
+  __syncthreads();
+  for (int e = t; e < E; e += 256) {
+    seg[e] = base[e];
+    int run = base[e];
+    for (int k = 0; k < nblk; k++) {
+      const int c = bcount[(int64_t)k * E + e];
+      bcount[(int64_t)k * E + e] = run;
+      run += c;
+    }
+    for (int i = 0; i < tb[e + 1] - tb[e]; i++) {
+      tiles[2 * (tb[e] + i)] = e;
+      tiles[2 * (tb[e] + i) + 1] = i;
+    }
+  }
+  if (t == 0) seg[E] = base[E];
+}
+
+__global__ __launch_bounds__(kBlk) void moe_place_kernel(const int* __restrict__ best, const int* __restrict__ rank,
+                                                         const int* __restrict__ boff, int* __restrict__ perm, int M,
+                                                         int E) {
+  const int tok = blockIdx.x * kBlk + threadIdx.x;
+  if (tok >= M) return;
+  const int e = best[tok];
+  if (e < 0) return;
+  perm[boff[(int64_t)blockIdx.x * E + e] + rank[tok]] = tok;
+}
+
+__global__ void zero_rows_kernel(const int* __restrict__ best, float* __restrict__ out, int M, int D) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * D) return;
+  if (best[i / D] < 0) out[i] = 0.f;
+}
+
+}  // namespace
+
+size_t moe_work_ints(int64_t M, int64_t E) {
+  const int64_t nblk = ceil_div(M, kBlk);
+  // best, rank, perm: 3M; bcount: nblk*E; seg: E+1; tiles: 2*(M/128+E+1); ntiles: 1
+  return (size_t)(3 * M + nblk * E + (E + 1) + 2 * (ceil_div(M, 128) + E + 1) + 1);
+}
+
+int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
+                     int64_t E, hipStream_t s) {
+  if (M <= 0) return 0;
+  if (E > 256 || M > INT32_MAX / 2) {
+    set_error("moe: more than 256 experts or too many tokens");
+    return -1;
+  }
+  const dim3 g1((unsigned)ceil_div(M, kTok));
+  const int m = (int)M, d = (int)D, e = (int)E;
+  if (E <= 64) hipLaunchKernelGGL(moe_router_kernel<1>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+  else if (E <= 128) hipLaunchKernelGGL(moe_router_kernel<2>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+  else hipLaunchKernelGGL(moe_router_kernel<4>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+  NSH_LAUNCHED();
+  const int nblk = (int)ceil_div(M, kBlk);
+  hipLaunchKernelGGL(moe_rank_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, m, e);
+  NSH_LAUNCHED();
+  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
+  NSH_LAUNCHED();
+  hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, w.perm, m, e);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+int launch_moe_experts(const float* x, const float* We1, const float* We2, const MoeWork& w, float* out, int64_t M,
+                       int64_t D, int64_t H, int64_t E, hipStream_t s) {
+  if (M <= 0) return 0;
+  // hidden[pos] = GELU(x[perm[pos]] . We1[e])   (expert-sorted rows)
+  GemmArgs g;
+  g.A = x; g.B = We1; g.C = w.hidden;
+  g.M = (int)M; g.N = (int)H; g.K = (int)D;
+  g.lda = D; g.ldb = H; g.ldc = H;
+  g.act = kActGelu;
+  g.a_rows = w.perm;
+  g.groups = (int)E; g.seg = w.seg; g.tiles = w.tiles; g.ntiles = w.ntiles; g.sBg = D * H;
+  if (launch_gemm_ex(g, false, false, 1, s) != 0) return -1;
+  // out[perm[pos]] = p[perm[pos]] * (hidden[pos] . We2[e])
+  GemmArgs g2 = g;
+  g2.A = w.hidden; g2.B = We2; g2.C = out;
+  g2.N = (int)D; g2.K = (int)H;
+  g2.lda = H; g2.ldb = D; g2.ldc = D;
+  g2.act = kActId;
+  g2.a_rows = nullptr;
+  g2.c_rows = w.perm;
+  g2.row_scale = w.prob;
+  g2.sBg = H * D;
+  if (launch_gemm_ex(g2, false, false, 1, s) != 0) return -1;
+  // tokens without a live expert
+  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)ceil_div(M * D, 256)), dim3(256), 0, s, w.best, out, (int)M,
+                     (int)D);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+}  // namespace nship

@@ -1,0 +1,376 @@
+// Row-wise and gather/scatter kernels (HBM-bound), wave64 throughout.
+//
+//   embedding gather        ns_embedding        codegen.cpp:1711-1718
+//   LayerNorm forward       ns_layernorm        codegen.cpp:1280-1291
+//   LayerNorm backward      ns_layernorm_grad   codegen.cpp:1346-1371
+//   cross-entropy + seed    ns_cross_entropy / ns_loss_grad  codegen.cpp:1582-1613
+//   activation backward     ns_act_grad         codegen.cpp:1340-1343
+//   embedding weight grad   ns_embedding_grad_w codegen.cpp:1374-1383
+//
+// One wave owns one row: the row is loaded once into registers (float4,
+// coalesced), reduced with xor-shuffles, and written once, so each kernel
+// moves the algorithmic minimum of bytes.  The embedding gradient is
+// deterministic and bit-exact: tokens are grouped by row with a stable
+// counting sort and each output element sums its tokens in token order, as
+// the reference's sequential scatter-add does.
+#include "common.h"
+#include "kernels.h"
+
+namespace nship {
+
+// Resolved embedding row of a float index, -1 if out of range.  Same
+// predicate as C truncation followed by the reference's range check, but
+// defined for NaN and huge values (which x86 turns into INT64_MIN).
+__device__ __forceinline__ int64_t emb_row(float f, int64_t V) {
+  if (!(f > -1.0f) || !(f < (float)V)) return -1;
+  const int64_t k = (int64_t)f;
+  return (k < 0 || k >= V) ? -1 : k;
+}
+
+// ---- embedding gather ----------------------------------------------------
+// One wave per output row; D % 4 == 0 uses float4.
+template <bool VEC>
+__global__ __launch_bounds__(256) void embedding_kernel(const float* __restrict__ W, const float* __restrict__ idx,
+                                                        float* __restrict__ out, int64_t n, int64_t V, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n) return;
+  int64_t k = emb_row(idx[row], V);
+  if (k < 0) k = 0;
+  const float* src = W + k * D;
+  float* dst = out + row * D;
+  if (VEC) {
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    for (int64_t j = lane; j < D / 4; j += 64) d4[j] = s4[j];
+  } else {
+    for (int64_t j = lane; j < D; j += 64) dst[j] = src[j];
+  }
+}
+
+int launch_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D, hipStream_t s) {
+  if (n <= 0) return 0;
+  const dim3 grid((unsigned)ceil_div(n, 4));
+  const bool vec = (D % 4 == 0) && ((uintptr_t)W % 16 == 0) && ((uintptr_t)out % 16 == 0);
+  if (vec) hipLaunchKernelGGL(embedding_kernel<true>, grid, dim3(256), 0, s, W, idx, out, n, V, D);
+  else hipLaunchKernelGGL(embedding_kernel<false>, grid, dim3(256), 0, s, W, idx, out, n, V, D);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ---- LayerNorm forward -----------------------------------------------------
+// Row held in registers: NV float4 per lane covers up to 256*NV columns.
+template <int NV>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        int64_t rows, int last) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * last;
+  float4 v[NV];
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c = (lane + 64 * i) * 4;
+    v[i] = c < last ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  }
+  const float mean = wave_sum(sum) / (float)last;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c = (lane + 64 * i) * 4;
+    if (c < last) {
+      const float a = v[i].x - mean, b = v[i].y - mean, d = v[i].z - mean, e = v[i].w - mean;
+      sq += (a * a + b * b) + (d * d + e * e);
+    }
+  }
+  const float var = wave_sum(sq) / (float)last;
+  const float inv = 1.f / sqrtf(var + 1e-5f);
+  float* yr = y + r * last;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c = (lane + 64 * i) * 4;
+    if (c < last)
+      *reinterpret_cast<float4*>(yr + c) =
+          make_float4((v[i].x - mean) * inv, (v[i].y - mean) * inv, (v[i].z - mean) * inv, (v[i].w - mean) * inv);
+  }
+}
+
+// Any width: three streaming passes.
+__global__ __launch_bounds__(256) void layernorm_any_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                            int64_t rows, int last) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * last;
+  float sum = 0.f;
+  for (int c = lane; c < last; c += 64) sum += xr[c];
+  const float mean = wave_sum(sum) / (float)last;
+  float sq = 0.f;
+  for (int c = lane; c < last; c += 64) { const float a = xr[c] - mean; sq += a * a; }
+  const float inv = 1.f / sqrtf(wave_sum(sq) / (float)last + 1e-5f);
+  float* yr = y + r * last;
+  for (int c = lane; c < last; c += 64) yr[c] = (xr[c] - mean) * inv;
+}
+
+int launch_layernorm(const float* x, float* y, int64_t rows, int64_t last, hipStream_t s) {
+  if (rows <= 0) return 0;
+  const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
+  const bool vec = last % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
+  const int L = (int)last;
+  if (vec && last <= 256) hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 512) hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 1024) hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 2048) hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, s, x, y, rows, L);
+  else hipLaunchKernelGGL(layernorm_any_kernel, grid, block, 0, s, x, y, rows, L);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ---- LayerNorm backward ------------------------------------------------------
+// dx = (d - mean(d) - (x - mean(x)) * mean((x - mean(x)) * d)) / sqrt(var + eps),
+// exactly the reference's formula (its projection term has no 1/(var+eps)).
+__global__ __launch_bounds__(256) void layernorm_grad_kernel(const float* __restrict__ dout,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ dx, int64_t rows, int last) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * last;
+  const float* dr = dout + r * last;
+  float sx = 0.f, sd = 0.f;
+  for (int c = lane; c < last; c += 64) { sx += xr[c]; sd += dr[c]; }
+  const float mx = wave_sum(sx) / (float)last;
+  const float md = wave_sum(sd) / (float)last;
+  float sv = 0.f, sg = 0.f;
+  for (int c = lane; c < last; c += 64) {
+    const float a = xr[c] - mx;
+    sv += a * a;
+    sg += a * dr[c];
+  }
+  const float var = wave_sum(sv) / (float)last;
+  const float gamma = wave_sum(sg) / (float)last;
+  const float inv = 1.f / sqrtf(var + 1e-5f);
+  float* o = dx + r * last;
+  for (int c = lane; c < last; c += 64) o[c] = (dr[c] - md - (xr[c] - mx) * gamma) * inv;
+}
+
+int launch_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last, hipStream_t s) {
+  if (rows <= 0) return 0;
+  hipLaunchKernelGGL(layernorm_grad_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, dout, x, dx, rows,
+                     (int)last);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ---- softmax cross-entropy: loss terms and the gradient seed in one pass ----
+// Per row: max, sum of exp, then for every column p = exp(x - max) / sum,
+// grad = (p - y) / rows, and -log(p) summed over columns with y > 0 into
+// row_loss[row].  Columns are visited twice (max, then exp/sum) from
+// registers when the row fits, else from memory.
+__global__ __launch_bounds__(256) void softmax_xent_kernel(const float* __restrict__ logits,
+                                                           const float* __restrict__ labels,
+                                                           float* __restrict__ grad, float* __restrict__ row_loss,
+                                                           int64_t rows, int64_t C, int write_grad) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = logits + r * C;
+  const float* yr = labels + r * C;
+  float mx = -INFINITY;
+  for (int64_t c = lane; c < C; c += 64) mx = fmaxf(mx, xr[c]);
+  mx = wave_max(mx);
+  float s = 0.f;
+  for (int64_t c = lane; c < C; c += 64) s += expf(xr[c] - mx);
+  s = wave_sum(s);
+  const float inv_rows = 1.f / (float)rows;
+  float loss = 0.f;
+  float* gr = grad + r * C;
+  for (int64_t c = lane; c < C; c += 64) {
+    const float p = expf(xr[c] - mx) / s;
+    const float y = yr[c];
+    if (y > 0.f) loss -= logf(p);
+    if (write_grad) gr[c] = (p - y) * inv_rows;
+  }
+  loss = wave_sum(loss);
+  if (lane == 0) row_loss[r] = loss;
+}
+
+// Deterministic single-workgroup sum of row losses / rows.
+__global__ __launch_bounds__(256) void mean_loss_kernel(const float* __restrict__ row_loss, int64_t rows,
+                                                        float* __restrict__ out) {
+  __shared__ float part[4];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < rows; i += 256) s += row_loss[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = ((part[0] + part[1]) + (part[2] + part[3])) / (float)rows;
+}
+
+int launch_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
+                        int64_t rows, int64_t C, bool write_grad, hipStream_t s) {
+  if (rows <= 0) return 0;
+  hipLaunchKernelGGL(softmax_xent_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, logits, labels, grad,
+                     row_loss, rows, C, write_grad ? 1 : 0);
+  NSH_LAUNCHED();
+  hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(256), 0, s, row_loss, rows, loss);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ---- activation backward (elementwise) ------------------------------------------
+__global__ void act_grad_kernel(const float* __restrict__ din, const float* __restrict__ pre,
+                                float* __restrict__ dout, int64_t n, int code) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dout[i] = din[i] * act_deriv(pre[i], code);
+}
+
+int launch_act_grad(const float* din, const float* pre, float* dout, int64_t n, int code, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(act_grad_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, din, pre, dout, n, code);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ---- embedding weight gradient --------------------------------------------------
+// Stable counting sort of tokens by row (counts, exclusive scan, in-order
+// placement), then one wave per vocabulary row sums its tokens' gradient
+// rows in token order and writes the dW row once (zero rows included).
+__global__ __launch_bounds__(256) void emb_count_kernel(const float* __restrict__ idx, int64_t n, int64_t V,
+                                                        int* __restrict__ count) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t r = emb_row(idx[i], V);
+  if (r >= 0) atomicAdd(&count[r], 1);
+}
+
+// Exclusive scan of V counts by one workgroup (V up to a few million).
+__global__ __launch_bounds__(1024) void exclusive_scan_kernel(const int* __restrict__ in, int* __restrict__ out,
+                                                              int64_t n) {
+  __shared__ int part[1024];
+  const int t = threadIdx.x;
+  const int64_t per = (n + 1023) / 1024;
+  const int64_t b = t * per, e = b + per < n ? b + per : n;
+  int s = 0;
+  for (int64_t i = b; i < e; i++) s += in[i];
+  part[t] = s;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int v = t >= o ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int run = part[t] - s;
+  for (int64_t i = b; i < e; i++) {
+    const int c = in[i];
+    out[i] = run;
+    run += c;
+  }
+  if (t == 1023) out[n] = part[1023];
+}
+
+// Placement: each token takes a slot of its row's segment through an atomic
+// cursor (arbitrary order); sorting every segment by token id then restores
+// token order, which is the stable order the reference's loop accumulates in.
+__global__ __launch_bounds__(256) void emb_place_kernel(const float* __restrict__ idx, int64_t n, int64_t V,
+                                                        const int* __restrict__ start, int* __restrict__ cursor,
+                                                        int* __restrict__ order) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t r = emb_row(idx[i], V);
+  if (r < 0) return;
+  const int pos = atomicAdd(&cursor[r], 1);
+  order[start[r] + pos] = (int)i;
+}
+
+// Sort the segments of rows [256*block, 256*block + 256).  Short segments
+// (<= 32 tokens) are insertion-sorted by their own thread; each longer one
+// is then ranked by the whole workgroup (rank = number of smaller token ids
+// in the segment, ids are distinct) through `tmp`.
+__global__ __launch_bounds__(256) void emb_sort_segments_kernel(const int* __restrict__ start, int64_t V,
+                                                                int* __restrict__ order, int* __restrict__ tmp) {
+  const int64_t r0 = (int64_t)blockIdx.x * 256;
+  const int64_t r = r0 + threadIdx.x;
+  if (r < V) {
+    const int b = start[r], e = start[r + 1];
+    if (e - b <= 32) {
+      for (int i = b + 1; i < e; i++) {
+        const int v = order[i];
+        int j = i - 1;
+        while (j >= b && order[j] > v) {
+          order[j + 1] = order[j];
+          j--;
+        }
+        order[j + 1] = v;
+      }
+    }
+  }
+  const int64_t r1 = r0 + 256 < V ? r0 + 256 : V;
+  for (int64_t q = r0; q < r1; q++) {
+    const int b = start[q], e = start[q + 1];
+    if (e - b <= 32) continue;  // uniform across the workgroup
+    for (int i = b + (int)threadIdx.x; i < e; i += 256) {
+      const int v = order[i];
+      int rank = 0;
+      for (int j = b; j < e; j++) rank += order[j] < v;
+      tmp[b + rank] = v;
+    }
+    __syncthreads();
+    for (int i = b + (int)threadIdx.x; i < e; i += 256) order[i] = tmp[i];
+    __syncthreads();
+  }
+}
+
+// dW[r,:] = sum over the row's tokens (ascending) of dout[token,:].
+__global__ __launch_bounds__(256) void emb_grad_rows_kernel(const float* __restrict__ dout,
+                                                            const int* __restrict__ start,
+                                                            const int* __restrict__ order, float* __restrict__ dW,
+                                                            int64_t V, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= V) return;
+  const int b = start[r], e = start[r + 1];
+  float* o = dW + r * D;
+  for (int64_t c = lane; c < D; c += 64) {
+    float acc = 0.f;
+    for (int t = b; t < e; t++) acc += dout[(int64_t)order[t] * D + c];
+    o[c] = acc;
+  }
+}
+
+// Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
+size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
+
+int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D, int* ws,
+                          hipStream_t s) {
+  int* count = ws;
+  int* start = ws + V;
+  int* cursor = ws + 2 * V + 1;
+  int* order = ws + 3 * V + 1;
+  int* tmp = order + n;
+  NSH_CHECK(hipMemsetAsync(count, 0, (size_t)V * sizeof(int), s));
+  NSH_CHECK(hipMemsetAsync(cursor, 0, (size_t)V * sizeof(int), s));
+  if (n > 0) {
+    hipLaunchKernelGGL(emb_count_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, idx, n, V, count);
+    NSH_LAUNCHED();
+  }
+  hipLaunchKernelGGL(exclusive_scan_kernel, dim3(1), dim3(1024), 0, s, count, start, V);
+  NSH_LAUNCHED();
+  if (n > 0) {
+    hipLaunchKernelGGL(emb_place_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, idx, n, V, start, cursor,
+                       order);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(emb_sort_segments_kernel, dim3((unsigned)ceil_div(V, 256)), dim3(256), 0, s, start, V, order,
+                       tmp);
+    NSH_LAUNCHED();
+  }
+  hipLaunchKernelGGL(emb_grad_rows_kernel, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, s, dout, start, order, dW,
+                     V, D);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+}  // namespace nship

@@ -61,6 +61,7 @@ struct ns_model {
   uint8_t* d_active = nullptr;
   std::mt19937 rng{0x9E3779B9u};  // codegen.cpp:2421
   int64_t lr_step = 0;
+  int64_t moe_last_m = 0;         // tokens routed by the last MoE forward
   std::vector<Buf> arena;         // per value id
   std::map<std::string, Buf> scratch;
   // profiling
@@ -138,10 +139,46 @@ __global__ void act_kernel(const float* __restrict__ x, float* __restrict__ y, i
 }
 
 // Per-call shapes and device pointers of every value of a function.
+struct AttnSaved {
+  float* qkv = nullptr;  // [3][BS][D]
+  float* ctx = nullptr;  // [BS][D] per-head outputs before the projection
+  float* lse = nullptr;  // [H][BS]
+  int64_t BS = 0;
+};
+
 struct Frame {
   std::vector<size_t> numel;
   std::vector<float*> ptr;
+  std::map<int, AttnSaved> attn;  // keyed by the attention input value id
 };
+
+float* scratch(ns_model* m, const std::string& key, size_t n) {
+  Buf& b = m->scratch[key];
+  if (ensure(b, n) != 0) return nullptr;
+  return b.p;
+}
+
+// MoE work arrays for M tokens (grow-only scratch).
+int moe_work(ns_model* m, int64_t M, MoeWork* w) {
+  const MoeInfo& q = m->plan->moe;
+  float* lg = scratch(m, "moe_logits", (size_t)(M * q.E));
+  float* pr = scratch(m, "moe_prob", (size_t)M);
+  float* hid = scratch(m, "moe_hidden", (size_t)(M * q.H));
+  int* iw = reinterpret_cast<int*>(scratch(m, "moe_ints", moe_work_ints(M, q.E)));
+  if (!lg || !pr || !hid || !iw) return -1;
+  const int64_t nblk = ceil_div(M, 256);
+  w->logits = lg;
+  w->prob = pr;
+  w->hidden = hid;
+  w->best = iw;
+  w->rank = iw + M;
+  w->perm = iw + 2 * M;
+  w->bcount = iw + 3 * M;
+  w->seg = w->bcount + nblk * q.E;
+  w->tiles = w->seg + q.E + 1;
+  w->ntiles = w->tiles + 2 * (ceil_div(M, 128) + q.E + 1);
+  return 0;
+}
 
 int bind_weights(ns_model* m, Frame& fr) {
   const Plan& P = *m->plan;
@@ -189,6 +226,81 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
         NSH_LAUNCHED();
       }
       return 0;
+    }
+    case Op::Embedding: {
+      const Value& W = P.vals[I.in[0]];
+      const size_t n = fr.numel[I.in[1]];
+      NSH_OUT(out, I.res, n * (size_t)W.cols);
+      Prof p(m, "embedding");
+      return launch_embedding(fr.ptr[I.in[0]], fr.ptr[I.in[1]], out, (int64_t)n, W.rows, W.cols, s);
+    }
+    case Op::LayerNorm: {
+      // row width: the result type's columns, else the input's
+      // (codegen.cpp:2021 forward, :2744-2751 train)
+      int64_t last = train ? F.width[I.in[0]] : (I.rt_cols > 0 ? I.rt_cols : F.width[I.in[0]]);
+      if (last <= 0) last = 1;
+      const size_t n = fr.numel[I.in[0]];
+      NSH_OUT(y, I.res, n);
+      Prof p(m, "layernorm");
+      return launch_layernorm(fr.ptr[I.in[0]], y, (int64_t)(n / (size_t)last), last, s);
+    }
+    case Op::Attention: {
+      const Value& Wq = P.vals[I.in[1]];
+      const int64_t D = Wq.rows, H = I.heads;
+      const int64_t BS = (int64_t)(fr.numel[I.in[0]] / (size_t)D);
+      NSH_OUT(out, I.res, (size_t)(BS * D));
+      const std::string key = std::to_string(I.res);
+      AttnSaved sv;
+      sv.BS = BS;
+      sv.qkv = scratch(m, "qkv" + key, (size_t)(3 * BS * D));
+      sv.ctx = scratch(m, "ctx" + key, (size_t)(BS * D));
+      sv.lse = scratch(m, "lse" + key, (size_t)(H * BS));
+      if (!sv.qkv || !sv.ctx || !sv.lse) return -1;
+      fr.attn[I.in[0]] = sv;
+      if (BS == 0) return 0;
+      // Q, K, V projections: one batched launch when the three weights are
+      // consecutive in the blob (they are for every Attention layer).
+      const Value& Wk = P.vals[I.in[2]];
+      const Value& Wv = P.vals[I.in[3]];
+      const bool packed = Wk.offset == Wq.offset + (size_t)(D * D) && Wv.offset == Wk.offset + (size_t)(D * D);
+      {
+        Prof p(m, "gemm");
+        GemmArgs g;
+        g.A = fr.ptr[I.in[0]];
+        g.M = (int)BS; g.N = (int)D; g.K = (int)D;
+        g.lda = D; g.ldb = D; g.ldc = D;
+        if (packed) {
+          g.B = fr.ptr[I.in[1]];
+          g.C = sv.qkv;
+          g.sA = 0; g.sB = D * D; g.sC = BS * D;
+          if (launch_gemm_ex(g, false, false, 3, s) != 0) return -1;
+        } else {
+          for (int j = 0; j < 3; j++) {
+            g.B = fr.ptr[I.in[1 + j]];
+            g.C = sv.qkv + j * BS * D;
+            if (launch_gemm_ex(g, false, false, 1, s) != 0) return -1;
+          }
+        }
+      }
+      {
+        Prof p(m, "attention_fwd");
+        if (launch_attention_fwd(sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, train ? sv.lse : nullptr, BS, D,
+                                 H, D, s) != 0)
+          return -1;
+      }
+      Prof p(m, "gemm");
+      return launch_gemm(sv.ctx, fr.ptr[I.in[4]], out, BS, D, D, D, D, D, false, false, 0, s);
+    }
+    case Op::Moe: {
+      const MoeInfo& q = P.moe;
+      const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)q.D);
+      NSH_OUT(out, I.res, (size_t)(M * q.D));
+      MoeWork w;
+      if (moe_work(m, M, &w) != 0) return -1;
+      Prof p(m, "moe");
+      if (launch_moe_route(fr.ptr[I.in[0]], fr.ptr[I.in[1]], m->d_active, w, M, q.D, q.E, s) != 0) return -1;
+      m->moe_last_m = M;
+      return launch_moe_experts(fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]], w, out, M, q.D, q.H, q.E, s);
     }
     case Op::Dropout:
       if (train) {
@@ -587,6 +699,21 @@ int nsh_profile_report(ns_model* m, char* buf, size_t len) {
   return 0;
 }
 
+int nsh_model_last_routing(ns_model* m, int32_t* best, float* prob, float* logits, size_t n) {
+  if (!m || !m->plan->moe.present || (size_t)m->moe_last_m != n) {
+    set_error("routing: no MoE forward of that size");
+    return -1;
+  }
+  if (sync(m) != 0) return -1;
+  const int64_t E = m->plan->moe.E;
+  MoeWork w;
+  if (moe_work(m, (int64_t)n, &w) != 0) return -1;
+  if (best) NSH_CHECK(hipMemcpy(best, w.best, n * sizeof(int32_t), hipMemcpyDeviceToHost));
+  if (prob) NSH_CHECK(hipMemcpy(prob, w.prob, n * sizeof(float), hipMemcpyDeviceToHost));
+  if (logits) NSH_CHECK(hipMemcpy(logits, w.logits, n * (size_t)E * sizeof(float), hipMemcpyDeviceToHost));
+  return 0;
+}
+
 // ---- kernels on device pointers ----------------------------------------------
 int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                 int64_t ldb, int64_t ldc, int transA, int transB, int act) {
@@ -597,6 +724,52 @@ int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, 
   if (launch_gemm(A, B, C, M, N, K, lda, ldb, ldc, transA != 0, transB != 0, act, nullptr) != 0) return -1;
   NSH_CHECK(hipStreamSynchronize(nullptr));
   return 0;
+}
+
+#define NSH_OP_DONE()                             \
+  do {                                            \
+    NSH_CHECK(hipStreamSynchronize(nullptr));     \
+    return 0;                                     \
+  } while (0)
+
+int nsh_op_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D) {
+  if (launch_embedding(W, idx, out, n, V, D, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+int nsh_op_layernorm(const float* x, float* y, int64_t rows, int64_t last) {
+  if (last <= 0 || launch_layernorm(x, y, rows, last, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+int nsh_op_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last) {
+  if (last <= 0 || launch_layernorm_grad(dout, x, dx, rows, last, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+int nsh_op_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
+                        int64_t rows, int64_t C) {
+  if (launch_softmax_xent(logits, labels, grad, row_loss, loss, rows, C, grad != nullptr, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+int nsh_op_act_grad(const float* din, const float* pre, float* dout, int64_t n, int act) {
+  if (launch_act_grad(din, pre, dout, n, act, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V) { return embedding_grad_workspace(n, V) * sizeof(int); }
+
+int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                          void* workspace) {
+  if (!workspace || launch_embedding_grad(dout, idx, dW, n, V, D, (int*)workspace, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
+                         int64_t D, int64_t H) {
+  if (launch_attention_fwd(Q, K, V, ctx, lse, S, D, H, D, nullptr) != 0) return -1;
+  NSH_OP_DONE();
 }
 
 }  // extern "C"

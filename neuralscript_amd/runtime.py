@@ -70,6 +70,15 @@ def lib():
             "nsh_profile_reset": (ci, [vp]),
             "nsh_profile_report": (ci, [vp, ctypes.c_char_p, sz]),
             "nsh_op_gemm": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, ci]),
+            "nsh_model_last_routing": (ci, [vp, vp, vp, vp, sz]),
+            "nsh_op_embedding": (ci, [vp, vp, vp, i64, i64, i64]),
+            "nsh_op_layernorm": (ci, [vp, vp, i64, i64]),
+            "nsh_op_layernorm_grad": (ci, [vp, vp, vp, i64, i64]),
+            "nsh_op_softmax_xent": (ci, [vp, vp, vp, vp, vp, i64, i64]),
+            "nsh_op_act_grad": (ci, [vp, vp, vp, i64, ci]),
+            "nsh_op_embedding_grad_workspace": (sz, [i64, i64]),
+            "nsh_op_embedding_grad": (ci, [vp, vp, vp, i64, i64, i64, vp]),
+            "nsh_op_attention_fwd": (ci, [vp, vp, vp, vp, vp, i64, i64, i64]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -217,6 +226,14 @@ class Model:
                                        loss.ctypes.data_as(_f32p)), "objective_loss")
         return loss[0]
 
+    def last_routing(self, n, E):
+        best = np.empty(n, dtype=np.int32)
+        prob = np.empty(n, dtype=np.float32)
+        lg = np.empty(n * E, dtype=np.float32)
+        check(lib().nsh_model_last_routing(self.h, best.ctypes.data, prob.ctypes.data, lg.ctypes.data, n),
+              "last_routing")
+        return best, prob, lg
+
     def profile(self, on=True):
         check(lib().nsh_profile_enable(self.h, 1 if on else 0), "profile_enable")
 
@@ -257,3 +274,13 @@ def bundled_nets():
 def gemm(dA, dB, dC, M, N, K, lda, ldb, ldc, transA=False, transB=False, act=0):
     check(lib().nsh_op_gemm(dA.ptr, dB.ptr, dC.ptr, M, N, K, lda, ldb, ldc, int(transA), int(transB), act),
           "gemm")
+
+
+def _p(d):
+    return d.ptr if d is not None else None
+
+
+def op(name, *args):
+    """Call nsh_op_<name> with DeviceArray / scalar arguments."""
+    conv = [_p(a) if isinstance(a, DeviceArray) or a is None else a for a in args]
+    check(getattr(lib(), "nsh_op_" + name)(*conv), name)

@@ -15,7 +15,7 @@
  * output elements (loop interchange, row blocking, threads), which leaves
  * every result bit-identical to the emitted scalar code.  The reference's own
  * emitted code, compiled from its sources into oracle/_ref/, pins this
- * bitwise (tests/test_oracle_vs_ref.py).
+ * bitwise (tests/test_oracle.py).
  */
 #include <math.h>
 #include <stdint.h>
@@ -594,6 +594,31 @@ EXPORT void or_moe_gate_logits(const float* x, const float* Wg, float* logits,
             for (int64_t k = 0; k < D; k++) a += x[(size_t)i * D + k] * Wg[k * E + e];
             logits[(size_t)i * E + e] = a;
         }
+}
+
+/* Routing only (best expert, its probability, raw logits) of every token:
+ * the router part of ns_moe_fwd, codegen.cpp:1921-1936. */
+EXPORT void or_moe_route(const float* x, const float* Wg, const uint8_t* active, int64_t* best_out,
+                         float* prob_out, float* logits_out, int64_t M, int64_t D, int64_t E) {
+#pragma omp parallel
+    {
+        float* lg = (float*)malloc((size_t)E * sizeof(float));
+#pragma omp for schedule(static)
+        for (int64_t i = 0; i < M; i++) {
+            const float* xi = x + (size_t)i * D;
+            if (logits_out)
+                for (int64_t e = 0; e < E; e++) {
+                    float a = 0.f;
+                    for (int64_t k = 0; k < D; k++) a += xi[k] * Wg[k * E + e];
+                    logits_out[(size_t)i * E + e] = a;
+                }
+            float sum;
+            const int64_t b = moe_route(xi, Wg, active, lg, NULL, &sum, D, E);
+            best_out[i] = b;
+            prob_out[i] = (b >= 0 && sum > 0.f) ? lg[b] / sum : 0.f;
+        }
+        free(lg);
+    }
 }
 
 /* out = p_best * GELU(x We1[best]) We2[best]; ns_moe_fwd codegen.cpp:1915-1945.

@@ -39,7 +39,7 @@ def build_command():
     src = os.path.join(_HERE, "ns_oracle.c")
     # -ffp-contract=off: the reference's emitted code never fuses a multiply
     # and an add (g++ -O2 -std=c++11 on x86-64 has no FMA), so neither may we.
-    return ["gcc", "-O3", "-march=x86-64-v2", "-ffp-contract=off", "-fno-fast-math",
+    return ["gcc", "-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math",
             "-fopenmp", "-fPIC", "-shared", src, "-o", LIB_PATH, "-lm"]
 
 
@@ -69,6 +69,7 @@ def lib():
             "or_attention_bwd": (None, [_f32p] * 11 + [i64, i64, i64]),
             "or_moe_gate_logits": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
             "or_moe_fwd": (None, [_f32p] * 4 + [_u8p, _f32p, _i64p, _f32p, i64, i64, i64, i64]),
+            "or_moe_route": (None, [_f32p, _f32p, _u8p, _i64p, _f32p, _f32p, i64, i64, i64]),
             "or_moe_bwd": (None, [_f32p] * 5 + [_u8p] + [_f32p] * 4 + [i64, i64, i64, i64]),
             "or_orthonom": (None, [_f32p, i64, i64]),
             "or_muon_step": (None, [_f32p, _f32p, i64, i64, cf]),
@@ -229,6 +230,14 @@ def moe_fwd(x, Wg, We1, We2, active, M, D, H, E):
     lib().or_moe_fwd(fp(x), fp(Wg), fp(We1), fp(We2), up(active), fp(out), ip(best), fp(prob),
                      M, D, H, E)
     return out, best, prob
+
+
+def moe_route(x, Wg, active, M, D, E, want_logits=False):
+    best = np.empty(M, dtype=np.int64)
+    prob = empty(M)
+    lg = empty(M * E) if want_logits else None
+    lib().or_moe_route(fp(x), fp(Wg), up(active), ip(best), fp(prob), fp(lg), M, D, E)
+    return best, prob, lg
 
 
 def moe_bwd(dout, x, Wg, We1, We2, active, M, D, H, E):

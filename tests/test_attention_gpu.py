@@ -1,0 +1,86 @@
+"""Attention core (flash forward) against the oracle's exact-softmax
+attention, and the c3 network."""
+import numpy as np
+import pytest
+
+import helpers
+import oracle
+from neuralscript_amd import runtime, synth, workloads
+from neuralscript_amd.runtime import DeviceArray as DA
+
+pytestmark = pytest.mark.gpu
+
+
+def core_ref(Q, K, V, S, D, H):
+    """The attention core (scores, softmax, P V) in float64; the layer-level
+    tests below compare against the oracle's bit-faithful restatement."""
+    dk = D // H
+    out = np.zeros((S, D))
+    Qd, Kd, Vd = (a.reshape(S, D).astype(np.float64) for a in (Q, K, V))
+    for h in range(H):
+        sl = slice(h * dk, (h + 1) * dk)
+        s = Qd[:, sl] @ Kd[:, sl].T * (1.0 / np.sqrt(np.float32(dk)))
+        p = np.exp(s - s.max(1, keepdims=True))
+        out[:, sl] = (p / p.sum(1, keepdims=True)) @ Vd[:, sl]
+    return out
+
+
+@pytest.mark.parametrize("S,D,H", [(1, 64, 1), (100, 128, 2), (333, 64, 1), (1024, 1024, 16), (300, 64, 2),
+                                   (257, 16, 2), (90, 64, 8), (2048, 512, 8)])
+def test_attention_core_matches_float64(S, D, H):
+    print(f"attention core S={S} D={D} H={H}", flush=True)
+    Q, K, V = (synth.normal(S * 10 + i, S * D, 1.0) for i in range(3))
+    ctx, lse = DA(S * D), DA(S * H)
+    runtime.op("attention_fwd", DA.from_host(Q), DA.from_host(K), DA.from_host(V), ctx, lse, S, D, H)
+    helpers.assert_close(ctx.to_host(), core_ref(Q, K, V, S, D, H).ravel(), f"attention S={S} D={D} H={H}")
+
+
+def test_attention_layer_matches_oracle():
+    """Whole layer x -> (QKV projections, core, output projection) through a
+    network driver vs the oracle's ns_attention_fwd restatement."""
+    from golden.make_golden import case_inputs
+    g = np.load(f"{helpers.GOLDEN}/c3s.npz")
+    _, x, _ = case_inputs("c3s", 45, 105)
+    lib = runtime.net_lib("c3s")
+    m = lib.init(helpers.net_weights("c3s", 105))
+    out = lib.eval_infer(m, x)
+    lib.free(m)
+    helpers.assert_close(out, g["out"], "c3s forward vs reference fixture")
+
+
+@pytest.mark.parametrize("rows", [700, 1500])
+def test_c3_small_sequence_matches_oracle(rows):
+    ir = helpers.ir_text("c3s")
+    w = helpers.net_weights("c3s", rows, std=0.1)
+    net = oracle.Net(ir)
+    x = helpers.net_inputs(net, "c3s", rows, rows)
+    ref = oracle.Model(net, w).eval_infer(x)
+    lib = runtime.net_lib("c3s")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x)
+    lib.free(m)
+    helpers.assert_close(out, ref, f"c3s S={rows}")
+
+
+def test_c3_full_size_rows_match_oracle():
+    """Config 3 at full size: 16384 ids as one sequence, d_model 1024, 16
+    heads; the oracle recomputes 24 query rows (full K/V) and their LN."""
+    print("c3 full size", flush=True)
+    ir = helpers.ir_text("c3")
+    plan = runtime.Plan(ir)
+    shapes = workloads.ir_shapes(ir)
+    w = workloads.weights("c3", plan.layout(), shapes)
+    x = workloads.inputs("c3")
+    lib = runtime.net_lib("c3")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x).reshape(16384, 1024)
+    lib.free(m)
+    assert np.isfinite(out).all()
+    net = oracle.Net(ir)
+    o = net.offsets
+    emb = oracle.embedding(w[: 32000 * 1024], x, 32000, 1024)
+    Wq, Wk, Wv, Wo = (w[o[n]: o[n] + 1024 * 1024] for n in ("attn_q_w", "attn_k_w", "attn_v_w", "attn_o_w"))
+    rows = np.unique(np.linspace(0, 16383, 24).astype(np.int64))
+    att = oracle.attention_fwd_rows(emb, Wq, Wk, Wv, Wo, rows, 16384, 1024, 16)
+    ref = oracle.layernorm(att, 1024).reshape(len(rows), 1024)
+    helpers.assert_close(out[rows], ref, "c3 rows")
