@@ -87,6 +87,16 @@ int nsh_objective_loss(ns_model* m, const float* input, const float* labels,
 int nsh_eval_infer_device(ns_model* m, const float* d_input, float* d_output, size_t input_numel);
 int nsh_model_sync(ns_model* m);
 
+/* Device-resident training step (inputs and one-hot labels in device
+ * memory); loss_out is a host pointer (NULL: no wait, no loss). */
+int nsh_train_step_device(ns_model* m, const float* d_input, const float* d_labels, size_t input_numel,
+                          float* loss_out, float lr);
+
+/* Copy of IR value `name` (e.g. "g17", "attn8") as left by the most recent
+ * forward or training call; weights give their current values.  For
+ * per-instruction parity checks.  n must equal the value's element count. */
+int nsh_model_read_value(ns_model* m, const char* name, float* out, size_t n);
+
 /* Routing of the most recent MoE forward of n tokens: chosen expert (-1 if
  * none live), its probability, and the raw router logits [n, E].  Any output
  * may be NULL. */
@@ -143,6 +153,26 @@ int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_
  * of ns_attention_fwd, codegen.cpp:1724-1777. */
 int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
                          int64_t D, int64_t H);
+
+/* Modified Gram-Schmidt of g [r,c] over columns (r >= c) or rows (r < c),
+ * q = the orthonormal result in g's layout; ns_orthonom, codegen.cpp:1617-1633.
+ * workspace: device bytes from nsh_op_muon_workspace. */
+size_t nsh_op_muon_workspace(int64_t r, int64_t c);
+int nsh_op_orthonormalize(const float* g, float* q, int64_t r, int64_t c, void* workspace);
+
+/* Muon step of one matrix (momentum reset every step, so m = g):
+ * w -= lr sqrt(min(r,c)) MGS(g) + 0.01 lr w; codegen.cpp:3099-3107. */
+int nsh_op_muon_step(float* w, const float* g, int64_t r, int64_t c, float lr, void* workspace);
+
+/* Muon step of n matrices at once (the fused multi-tensor form the training
+ * step uses): w[i] [r[i], c[i]] updated with gradient g[i]. */
+size_t nsh_op_muon_multi_workspace(int n, const int64_t* r, const int64_t* c);
+int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64_t* r, const int64_t* c, float lr,
+                      void* workspace);
+
+/* AdamW step with step counter t (after increment), moments m, v updated in
+ * place; codegen.cpp:3108-3119. */
+int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr);
 
 #ifdef __cplusplus
 }

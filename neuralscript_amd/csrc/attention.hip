@@ -26,6 +26,12 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
+// x if `keep`, else zeros; component-wise (a select on the struct itself is
+// lowered through scratch memory).
+__device__ __forceinline__ float4 keep4(bool keep, float4 x) {
+  return make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
+}
+
 constexpr int kBQ = 128;  // queries per workgroup
 constexpr int kBK = 64;   // keys per tile
 
@@ -50,14 +56,14 @@ struct KVTile {
     for (int i = 0; i < kPer; i++) {
       const int idx = t + 256 * i;
       const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
+      // rows past the end load a clamped row and are zeroed by a select
       const int gk = key0 + key;
-      if (gk < S) {
-        k[i] = *reinterpret_cast<const float4*>(K + (int64_t)gk * ld + hcol + c);
-        v[i] = *reinterpret_cast<const float4*>(V + (int64_t)gk * ld + hcol + c);
-      } else {
-        k[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        v[i] = k[i];
-      }
+      const bool in = gk < S;
+      const int64_t row = in ? gk : S - 1;
+      const float4 a = *reinterpret_cast<const float4*>(K + row * ld + hcol + c);
+      const float4 b = *reinterpret_cast<const float4*>(V + row * ld + hcol + c);
+      k[i] = keep4(in, a);
+      v[i] = keep4(in, b);
     }
   }
   __device__ void store(float* __restrict__ ks, int t) const {
@@ -93,8 +99,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
   float qf[NS];
 #pragma unroll
   for (int g = 0; g < DK / 8; g++) {
-    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (qrow < S) x = *reinterpret_cast<const float4*>(Q + (int64_t)qrow * ld + hcol + 8 * g + 4 * kh);
+    const int64_t row = qrow < S ? qrow : S - 1;
+    const float4 x = keep4(qrow < S, *reinterpret_cast<const float4*>(Q + row * ld + hcol + 8 * g + 4 * kh));
     qf[4 * g] = x.x; qf[4 * g + 1] = x.y; qf[4 * g + 2] = x.z; qf[4 * g + 3] = x.w;
   }
 
@@ -235,6 +241,339 @@ __global__ __launch_bounds__(64) void attention_fwd_small_kernel(const float* __
   if (lse) lse[(int64_t)h * S + q] = mx * 1.4426950408889634f + log2f(sum);
 }
 
+
+// ============================================================================
+// Backward.  For one head, with c = scale * log2(e) and the forward's
+// lse[q] = log2 sum_k 2^(c S[q,k]):
+//   P = 2^(c S - lse),  dP = dO V^T,  dS = P (dP - delta),
+//   delta[q] = sum_d dO[q,d] O[q,d]  (= sum_k P dP, the reference's `dot`)
+//   dV = P^T dO,  dK = scale dS^T Q,  dQ = scale dS K
+// (ns_attention_bwd, codegen.cpp:1785-1907, computes the same quantities
+// with explicit S x S matrices.)  Two kernels, no atomics:
+//  * dk/dv: one workgroup per 128 keys (32 per wave) loops over query tiles;
+//    it forms S = Q K^T with the KEY as the lane column, so P and dS are the
+//    A operands of dV = P^T dO and dK = dS^T Q directly from registers.
+//  * dq: one workgroup per 128 queries loops over key tiles in the forward's
+//    transposed layout (lane = query): dS^T feeds dQ^T = K^T dS^T.
+// ============================================================================
+
+// delta[h*S + q] = sum_{d<DK} dO[q, h*DK + d] * O[q, h*DK + d]
+__global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict__ dO, const float* __restrict__ O,
+                                                         float* __restrict__ delta, int S, int H, int DK,
+                                                         int64_t ld) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (int64_t)S * H) return;
+  const int q = (int)(gid / H), h = (int)(gid % H);
+  const float* a = dO + (int64_t)q * ld + h * DK;
+  const float* b = O + (int64_t)q * ld + h * DK;
+  float acc = 0.f;
+  for (int d = 0; d < DK; d++) acc += a[d] * b[d];
+  delta[(int64_t)h * S + q] = acc;
+}
+
+template <int DK>
+struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
+  static constexpr int P = DK + 4;
+  static constexpr int kFloats = 2 * 64 * P + 128;
+  static constexpr int kPer = 64 * DK / 4 / 256;  // float4 per thread per matrix
+  float4 q[kPer], g[kPer];
+  float l = 0.f, d = 0.f;
+  __device__ void load(const float* __restrict__ Q, const float* __restrict__ dO, const float* __restrict__ lse,
+                       const float* __restrict__ delta, int64_t ld, int hcol, int hS, int q0, int S, int t) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      const int r = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
+      const int gq = q0 + r;
+      const bool in = gq < S;
+      const int64_t row = in ? gq : S - 1;
+      const float4 a = *reinterpret_cast<const float4*>(Q + row * ld + hcol + c);
+      const float4 b = *reinterpret_cast<const float4*>(dO + row * ld + hcol + c);
+      q[i] = keep4(in, a);
+      g[i] = keep4(in, b);
+    }
+    if (t < 64) {
+      const int gq = q0 + t;
+      // rows past the end: lse = +inf makes P = 0 there
+      l = gq < S ? lse[hS + gq] : INFINITY;
+      d = gq < S ? delta[hS + gq] : 0.f;
+    }
+  }
+  __device__ void store(float* __restrict__ sm, int t) const {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      const int r = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
+      *reinterpret_cast<float4*>(sm + r * P + c) = q[i];
+      *reinterpret_cast<float4*>(sm + 64 * P + r * P + c) = g[i];
+    }
+    if (t < 64) {
+      sm[2 * 64 * P + t] = l;
+      sm[2 * 64 * P + 64 + t] = d;
+    }
+  }
+};
+
+template <int DK>
+__global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                                                             const float* __restrict__ V, const float* __restrict__ dO,
+                                                             const float* __restrict__ lse,
+                                                             const float* __restrict__ delta, float* __restrict__ dK,
+                                                             float* __restrict__ dV, int S, int H, int64_t ld,
+                                                             float scale, float c_log2, int nkb) {
+  using Tile = QTile<DK>;
+  constexpr int NDB = DK / 32;
+  __shared__ __attribute__((aligned(16))) float sm[2 * Tile::kFloats];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int L = remap_xcd(blockIdx.x, nkb * H);
+  const int h = L / nkb, k0 = (L % nkb) * kBQ;
+  const int hcol = h * DK;
+  const int64_t hS = (int64_t)h * S;
+  const int key = k0 + w * 32 + l32;  // this lane's key (column of S)
+
+  // B operands: K and V rows of this lane's key, head dims 8g + 4kh + (0..3).
+  float kf[DK / 2], vf[DK / 2];
+#pragma unroll
+  for (int g = 0; g < DK / 8; g++) {
+    const int64_t row = key < S ? key : S - 1;
+    const float4 a = keep4(key < S, *reinterpret_cast<const float4*>(K + row * ld + hcol + 8 * g + 4 * kh));
+    const float4 b = keep4(key < S, *reinterpret_cast<const float4*>(V + row * ld + hcol + 8 * g + 4 * kh));
+    kf[4 * g] = a.x; kf[4 * g + 1] = a.y; kf[4 * g + 2] = a.z; kf[4 * g + 3] = a.w;
+    vf[4 * g] = b.x; vf[4 * g + 1] = b.y; vf[4 * g + 2] = b.z; vf[4 * g + 3] = b.w;
+  }
+  floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) { dk[d][v] = 0.f; dv[d][v] = 0.f; }
+
+  Tile tile;
+  const int nq = (S + 63) / 64;
+  tile.load(Q, dO, lse, delta, ld, hcol, (int)hS, 0, S, t);
+  tile.store(sm, t);
+  __syncthreads();
+  for (int it = 0; it < nq; it++) {
+    const int cur = it & 1;
+    const bool more = it + 1 < nq;
+    if (more) tile.load(Q, dO, lse, delta, ld, hcol, (int)hS, (it + 1) * 64, S, t);
+    const float* qs = sm + cur * Tile::kFloats;
+    const float* gs = qs + 64 * Tile::P;
+    const float* ls = qs + 2 * 64 * Tile::P;
+    const float* ds = ls + 64;
+#pragma unroll
+    for (int qb = 0; qb < 2; qb++) {
+      floatx16 sc, dp;
+#pragma unroll
+      for (int v = 0; v < 16; v++) { sc[v] = 0.f; dp[v] = 0.f; }
+#pragma unroll
+      for (int g = 0; g < DK / 8; g++) {
+        const float4 qa = *reinterpret_cast<const float4*>(qs + (qb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
+        const float4 ga = *reinterpret_cast<const float4*>(gs + (qb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.x, kf[4 * g + 0], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.y, kf[4 * g + 1], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.z, kf[4 * g + 2], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x2f32(qa.w, kf[4 * g + 3], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.x, vf[4 * g + 0], dp, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.y, vf[4 * g + 1], dp, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.z, vf[4 * g + 2], dp, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.w, vf[4 * g + 3], dp, 0, 0, 0);
+      }
+      // element v: query qb*32 + 8(v/4) + 4kh + v%4, key = this lane's
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int qr = qb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+        const float p = key < S ? exp2f(sc[v] * c_log2 - ls[qr]) : 0.f;
+        sc[v] = p;
+        dp[v] = p * (dp[v] - ds[qr]);
+      }
+      // dV += P^T dO, dK += dS^T Q: step s pairs query 8(s/4) + 4kh + s%4.
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const int qr = qb * 32 + 8 * (s >> 2) + 4 * kh + (s & 3);
+#pragma unroll
+        for (int d = 0; d < NDB; d++) {
+          dv[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(sc[s], gs[qr * Tile::P + d * 32 + l32], dv[d], 0, 0, 0);
+          dk[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(dp[s], qs[qr * Tile::P + d * 32 + l32], dk[d], 0, 0, 0);
+        }
+      }
+    }
+    if (more) tile.store(sm + (cur ^ 1) * Tile::kFloats, t);
+    __syncthreads();
+  }
+  // accumulator v of block d: key w*32 + 8(v/4) + 4kh + v%4, head dim d*32 + l32
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int kr = k0 + w * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+      if (kr < S) {
+        dK[(int64_t)kr * ld + hcol + d * 32 + l32] = dk[d][v] * scale;
+        dV[(int64_t)kr * ld + hcol + d * 32 + l32] = dv[d][v];
+      }
+    }
+}
+
+template <int DK>
+__global__ __launch_bounds__(256) void flash_bwd_dq_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                                                           const float* __restrict__ V, const float* __restrict__ dO,
+                                                           const float* __restrict__ lse,
+                                                           const float* __restrict__ delta, float* __restrict__ dQ,
+                                                           int S, int H, int64_t ld, float scale, float c_log2,
+                                                           int nqb) {
+  using Tile = KVTile<DK>;
+  constexpr int NDB = DK / 32;
+  __shared__ __attribute__((aligned(16))) float sm[2 * 2 * Tile::kFloats];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int L = remap_xcd(blockIdx.x, nqb * H);
+  const int h = L / nqb, q0 = (L % nqb) * kBQ;
+  const int hcol = h * DK;
+  const int qrow = q0 + w * 32 + l32;
+  float qf[DK / 2], gf[DK / 2];
+#pragma unroll
+  for (int g = 0; g < DK / 8; g++) {
+    const int64_t row = qrow < S ? qrow : S - 1;
+    const float4 a = keep4(qrow < S, *reinterpret_cast<const float4*>(Q + row * ld + hcol + 8 * g + 4 * kh));
+    const float4 b = keep4(qrow < S, *reinterpret_cast<const float4*>(dO + row * ld + hcol + 8 * g + 4 * kh));
+    qf[4 * g] = a.x; qf[4 * g + 1] = a.y; qf[4 * g + 2] = a.z; qf[4 * g + 3] = a.w;
+    gf[4 * g] = b.x; gf[4 * g + 1] = b.y; gf[4 * g + 2] = b.z; gf[4 * g + 3] = b.w;
+  }
+  const float lq = qrow < S ? lse[(int64_t)h * S + qrow] : INFINITY;
+  const float dq_delta = qrow < S ? delta[(int64_t)h * S + qrow] : 0.f;
+  floatx16 acc[NDB];
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[d][v] = 0.f;
+
+  Tile tile;
+  const int nkv = (S + kBK - 1) / kBK;
+  tile.load(K, V, ld, hcol, 0, S, t);
+  tile.store(sm, t);
+  __syncthreads();
+  for (int it = 0; it < nkv; it++) {
+    const int cur = it & 1;
+    const bool more = it + 1 < nkv;
+    if (more) tile.load(K, V, ld, hcol, (it + 1) * kBK, S, t);
+    const float* ks = sm + cur * 2 * Tile::kFloats;
+    const float* vs = ks + Tile::kFloats;
+    floatx16 sc[2], dp[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) { sc[kb][v] = 0.f; dp[kb][v] = 0.f; }
+#pragma unroll
+    for (int g = 0; g < DK / 8; g++)
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++) {
+        const float4 ka = *reinterpret_cast<const float4*>(ks + (kb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
+        const float4 va = *reinterpret_cast<const float4*>(vs + (kb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.x, qf[4 * g + 0], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.y, qf[4 * g + 1], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.z, qf[4 * g + 2], sc[kb], 0, 0, 0);
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka.w, qf[4 * g + 3], sc[kb], 0, 0, 0);
+        dp[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.x, gf[4 * g + 0], dp[kb], 0, 0, 0);
+        dp[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.y, gf[4 * g + 1], dp[kb], 0, 0, 0);
+        dp[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.z, gf[4 * g + 2], dp[kb], 0, 0, 0);
+        dp[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(va.w, gf[4 * g + 3], dp[kb], 0, 0, 0);
+      }
+    const int kbase = it * kBK;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int kr = kbase + kb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+        const float p = kr < S ? exp2f(sc[kb][v] * c_log2 - lq) : 0.f;
+        dp[kb][v] = p * (dp[kb][v] - dq_delta);
+      }
+    // dQ^T += K^T dS^T: step s of key block kb pairs key 8(s/4) + 4kh + s%4.
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        const int kr = kb * 32 + 8 * (s >> 2) + 4 * kh + (s & 3);
+#pragma unroll
+        for (int d = 0; d < NDB; d++)
+          acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[kr * Tile::P + d * 32 + l32], dp[kb][s], acc[d], 0, 0, 0);
+      }
+    if (more) tile.store(sm + (cur ^ 1) * 2 * Tile::kFloats, t);
+    __syncthreads();
+  }
+  // dQ^T (d, query) -> LDS [query][d] -> rows of dQ
+  float* T = sm + w * 32 * (DK + 1);
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) T[l32 * (DK + 1) + d * 32 + 8 * (v >> 2) + 4 * kh + (v & 3)] = acc[d][v] * scale;
+  __syncthreads();
+  for (int r = 0; r < 32; r++) {
+    const int q = q0 + w * 32 + r;
+    if (q >= S) break;
+    for (int c = lane; c < DK; c += 64) dQ[(int64_t)q * ld + hcol + c] = T[r * (DK + 1) + c];
+  }
+}
+
+// Any head size up to 128 (test networks): one thread per (row, head).
+// Pass 1 (per query): dQ.  Pass 2 (per key): dK, dV.
+__global__ __launch_bounds__(64) void attn_bwd_small_q_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+                                                              const float* __restrict__ V,
+                                                              const float* __restrict__ dO,
+                                                              const float* __restrict__ lse,
+                                                              const float* __restrict__ delta, float* __restrict__ dQ,
+                                                              int S, int H, int DK, int64_t ld, float scale,
+                                                              float c_log2) {
+  const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (gid >= (int64_t)S * H) return;
+  const int q = (int)(gid / H), h = (int)(gid % H);
+  const float* qr = Q + (int64_t)q * ld + h * DK;
+  const float* gr = dO + (int64_t)q * ld + h * DK;
+  const float lq = lse[(int64_t)h * S + q], dl = delta[(int64_t)h * S + q];
+  float acc[128];
+  for (int d = 0; d < DK; d++) acc[d] = 0.f;
+  for (int j = 0; j < S; j++) {
+    const float* kr = K + (int64_t)j * ld + h * DK;
+    const float* vr = V + (int64_t)j * ld + h * DK;
+    float s = 0.f, dp = 0.f;
+    for (int d = 0; d < DK; d++) { s += qr[d] * kr[d]; dp += gr[d] * vr[d]; }
+    const float ds = exp2f(s * c_log2 - lq) * (dp - dl);
+    for (int d = 0; d < DK; d++) acc[d] += ds * kr[d];
+  }
+  float* o = dQ + (int64_t)q * ld + h * DK;
+  for (int d = 0; d < DK; d++) o[d] = acc[d] * scale;
+}
+
+__global__ __launch_bounds__(64) void attn_bwd_small_kv_kernel(const float* __restrict__ Q,
+                                                               const float* __restrict__ K,
+                                                               const float* __restrict__ V,
+                                                               const float* __restrict__ dO,
+                                                               const float* __restrict__ lse,
+                                                               const float* __restrict__ delta,
+                                                               float* __restrict__ dK, float* __restrict__ dV, int S,
+                                                               int H, int DK, int64_t ld, float scale,
+                                                               float c_log2) {
+  const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (gid >= (int64_t)S * H) return;
+  const int j = (int)(gid / H), h = (int)(gid % H);
+  const float* kr = K + (int64_t)j * ld + h * DK;
+  const float* vr = V + (int64_t)j * ld + h * DK;
+  float ak[128], av[128];
+  for (int d = 0; d < DK; d++) { ak[d] = 0.f; av[d] = 0.f; }
+  for (int q = 0; q < S; q++) {
+    const float* qr = Q + (int64_t)q * ld + h * DK;
+    const float* gr = dO + (int64_t)q * ld + h * DK;
+    float s = 0.f, dp = 0.f;
+    for (int d = 0; d < DK; d++) { s += qr[d] * kr[d]; dp += gr[d] * vr[d]; }
+    const float p = exp2f(s * c_log2 - lse[(int64_t)h * S + q]);
+    const float ds = p * (dp - delta[(int64_t)h * S + q]);
+    for (int d = 0; d < DK; d++) { av[d] += p * gr[d]; ak[d] += ds * qr[d]; }
+  }
+  for (int d = 0; d < DK; d++) {
+    dK[(int64_t)j * ld + h * DK + d] = ak[d] * scale;
+    dV[(int64_t)j * ld + h * DK + d] = av[d];
+  }
+}
+
 }  // namespace
 
 int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,
@@ -262,6 +601,50 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
     }
     hipLaunchKernelGGL(attention_fwd_small_kernel, dim3((unsigned)ceil_div(S * H, 64)), dim3(64), 0, s, Q, K, V, ctx,
                        lse, (int)S, (int)H, (int)DK, ld, scale);
+  }
+  NSH_LAUNCHED();
+  return 0;
+}
+
+int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                         const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
+                         int64_t H, int64_t ld, hipStream_t s) {
+  if (S <= 0) return 0;
+  if (H <= 0 || D % H != 0 || S > INT32_MAX) {
+    set_error("attention backward: bad shape");
+    return -1;
+  }
+  const int64_t DK = D / H;
+  if (DK > 128) {
+    set_error("attention: head size above 128 is not supported");
+    return -1;
+  }
+  const float scale = 1.0f / sqrtf((float)DK);
+  const float cl2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)ceil_div(S * H, 256)), dim3(256), 0, s, dO, O, delta, (int)S,
+                     (int)H, (int)DK, ld);
+  NSH_LAUNCHED();
+  const bool aligned = ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)dO) % 16 == 0;
+  if (aligned && (DK == 64 || DK == 32)) {
+    const int nb = (int)ceil_div(S, kBQ);
+    const dim3 grid(nb * (unsigned)H), block(256);
+    if (DK == 64) {
+      hipLaunchKernelGGL(flash_bwd_dkdv_kernel<64>, grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
+                         ld, scale, cl2, nb);
+      hipLaunchKernelGGL(flash_bwd_dq_kernel<64>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,
+                         scale, cl2, nb);
+    } else {
+      hipLaunchKernelGGL(flash_bwd_dkdv_kernel<32>, grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
+                         ld, scale, cl2, nb);
+      hipLaunchKernelGGL(flash_bwd_dq_kernel<32>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,
+                         scale, cl2, nb);
+    }
+  } else {
+    const dim3 grid((unsigned)ceil_div(S * H, 64));
+    hipLaunchKernelGGL(attn_bwd_small_q_kernel, grid, dim3(64), 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H,
+                       (int)DK, ld, scale, cl2);
+    hipLaunchKernelGGL(attn_bwd_small_kv_kernel, grid, dim3(64), 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
+                       (int)DK, ld, scale, cl2);
   }
   NSH_LAUNCHED();
   return 0;

@@ -34,7 +34,7 @@ constexpr int kWave = 64;
 // Activation codes shared with the reference's ns_act2 switch
 // (codegen.cpp:1244-1255): 0 id, 1 relu, 2 leaky, 3 sigmoid, 4 tanh,
 // 5 silu, 6 gelu.
-enum Act : int { kActId = 0, kActRelu, kActLeaky, kActSigmoid, kActTanh, kActSilu, kActGelu };
+enum Act : int { kActId = 0, kActRelu, kActLeaky, kActSigmoid, kActTanh, kActSilu, kActGelu, kActGeluMoe };
 
 __device__ __forceinline__ float act_apply(float x, int code) {
   switch (code) {
@@ -44,6 +44,8 @@ __device__ __forceinline__ float act_apply(float x, int code) {
     case kActTanh: return tanhf(x);
     case kActSilu: return x / (1.f + expf(-x));
     case kActGelu: return 0.5f * x * (1.f + erff(x / 1.41421356f));
+    // the MoE expert's spelling of GELU (codegen.cpp:1937)
+    case kActGeluMoe: return 0.5f * x * (1.f + erff(x * 0.7071067811865476f));
     default: return x;
   }
 }
@@ -61,6 +63,9 @@ __device__ __forceinline__ float act_deriv(float x, int code) {
       float p = 0.5f * (1.f + erff(u));
       return p + x * expf(-u * u) / 2.50662827f;
     }
+    // the MoE expert's spelling (codegen.cpp:1427-1428)
+    case kActGeluMoe:
+      return 0.5f * (1.f + erff(x * 0.7071067811865476f)) + x * expf(-x * x * 0.5f) * 0.3989422804014327f;
     default: return 1.f;
   }
 }

@@ -152,6 +152,12 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
   const float* __restrict__ B = g.B + (int64_t)blockIdx.y * g.sB;
   float* __restrict__ C = g.C + (int64_t)blockIdx.y * g.sC;
   int m_end = M;
+  // K-grouped: group blockIdx.y contracts over k in [kseg[y], kseg[y+1]).
+  int kbeg = 0, kend = K;
+  if (g.kseg) {
+    kbeg = g.kseg[blockIdx.y];
+    kend = g.kseg[blockIdx.y + 1];
+  }
   constexpr bool AKC = !TA, BKC = TB;
   constexpr int ASZ = TileLayout<AKC>::kSize, BSZ = TileLayout<BKC>::kSize;
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
@@ -190,9 +196,9 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
 
   Stage<AKC, VEC> sa;
   Stage<BKC, VEC> sb;
-  const int nk = (K + BK - 1) / BK;
-  sa.load(A, lda, m0, m_end, 0, K, t, g.a_rows);
-  sb.load(B, ldb, n0, N, 0, K, t);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  sa.load(A, lda, m0, m_end, kbeg, kend, t, g.a_rows);
+  sb.load(B, ldb, n0, N, kbeg, kend, t);
   sa.store(smem, t);
   sb.store(smem + ASZ, t);
   __syncthreads();
@@ -201,8 +207,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      sa.load(A, lda, m0, m_end, (kt + 1) * BK, K, t, g.a_rows);
-      sb.load(B, ldb, n0, N, (kt + 1) * BK, K, t);
+      sa.load(A, lda, m0, m_end, kbeg + (kt + 1) * BK, kend, t, g.a_rows);
+      sb.load(B, ldb, n0, N, kbeg + (kt + 1) * BK, kend, t);
     }
     const float* as = smem + cur * (ASZ + BSZ);
     const float* bs = as + ASZ;
@@ -259,8 +265,12 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   GemmArgs g = in;
   // float4 staging needs each operand's contiguous extent, leading dimension,
   // batch stride and base to be 4-float aligned.
-  const bool va = aligned16(g.A) && g.lda % 4 == 0 && g.sA % 4 == 0 && ((tA ? g.M : g.K) % 4 == 0);
-  const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0);
+  // (K-grouped segments start anywhere, so a k-contiguous operand needs the
+  // scalar path there.)
+  const bool va = aligned16(g.A) && g.lda % 4 == 0 && g.sA % 4 == 0 && ((tA ? g.M : g.K) % 4 == 0) &&
+                  (tA || !g.kseg);
+  const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
+                  (!tB || !g.kseg);
   const bool vec = va && vb;
   g.tiles_m = (int)ceil_div(g.M, BM);
   g.tiles_n = (int)ceil_div(g.N, BN);

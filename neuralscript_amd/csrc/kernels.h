@@ -37,6 +37,9 @@ struct GemmArgs {
   const int* tiles = nullptr;
   const int* ntiles = nullptr;
   int64_t sBg = 0;
+  // K-grouped mode (kseg set): launch with batch = groups; group y contracts
+  // over k in [kseg[y], kseg[y+1]) and writes C + y * sC.
+  const int* kseg = nullptr;
   int tiles_m = 0, tiles_n = 0;    // filled by the launcher
 };
 
@@ -63,6 +66,32 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
 int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,
                          int64_t H, int64_t ld, hipStream_t s);
 
+// Backward of the core: dQ, dK, dV [S, D] (row pitch ld) from dO = d ctx, the
+// forward's ctx (O) and lse; delta: [H, S] workspace.
+int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                         const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
+                         int64_t H, int64_t ld, hipStream_t s);
+
+// optim.hip --------------------------------------------------------------------
+int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1t, float b2t,
+                 hipStream_t s);
+
+// One Muon matrix of an optimizer step (device-resident descriptor).
+struct MuonMat {
+  float* w;          // weight [r][c], updated in place
+  const float* g;    // gradient [r][c]
+  float* T;          // work: vectors contiguous, [C][R]
+  float* norms;      // [C]
+  int R, C;          // vector length, number of vectors
+  int transposed;    // r < c: the vectors are the rows of g
+  int nblk;          // workgroups of this matrix in each MGS step launch
+  float le, decay;   // lr * sqrt(min(r, c)), 0.01 * lr
+};
+int muon_blocks(int C);
+int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
+int launch_mgs_steps(const MuonMat* d_mats, int nmat, int total_blocks, int max_c, hipStream_t s);
+int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
+
 // moe.hip ----------------------------------------------------------------------
 struct MoeWork {
   float* logits;   // [M, E]  raw router logits (kept for tie reports)
@@ -75,11 +104,24 @@ struct MoeWork {
   int* tiles;      // [2 * (M/128 + E)] (expert, m-tile) pairs
   int* ntiles;     // [1]
   float* hidden;   // [M, H]  GELU(x We1[e]) in expert-sorted order
+  float* pre;      // [M, H]  x We1[e] before GELU (training only, else null)
+};
+struct MoeBwdWork {
+  float* dpre2;    // [M, H]
+  float* dH;       // [M, H]
+  float* hp;       // [M, H]  GELU(u) * p_best
+  float* dg;       // [M, E]  router logit gradient (token order)
+  float* xs;       // [M, D]  x in expert-sorted order
+  float* ds;       // [M, D]  dout in expert-sorted order
 };
 size_t moe_work_ints(int64_t M, int64_t E);   // int-sized words of all int arrays
 int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
                      int64_t E, hipStream_t s);
 int launch_moe_experts(const float* x, const float* We1, const float* We2, const MoeWork& w, float* out, int64_t M,
                        int64_t D, int64_t H, int64_t E, hipStream_t s);
+// dx / dWg / dWe1 / dWe2 (any may be null) from the forward's MoeWork (with pre).
+int launch_moe_backward(const float* x, const float* dout, const float* Wg, const float* We1, const float* We2,
+                        const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
+                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s);
 
 }  // namespace nship

@@ -173,6 +173,14 @@ __global__ __launch_bounds__(kBlk) void moe_place_kernel(const int* __restrict__
   perm[boff[(int64_t)blockIdx.x * E + e] + rank[tok]] = tok;
 }
 
+// hidden = GELU(pre) over the routed rows [0, *nrows) of [*, H].
+__global__ void gelu_rows_kernel(const float* __restrict__ pre, float* __restrict__ hid, const int* __restrict__ nrows,
+                                 int64_t H) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)(*nrows) * H) return;
+  hid[i] = act_apply(pre[i], kActGeluMoe);
+}
+
 __global__ void zero_rows_kernel(const int* __restrict__ best, float* __restrict__ out, int M, int D) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (int64_t)M * D) return;
@@ -218,10 +226,18 @@ int launch_moe_experts(const float* x, const float* We1, const float* We2, const
   g.A = x; g.B = We1; g.C = w.hidden;
   g.M = (int)M; g.N = (int)H; g.K = (int)D;
   g.lda = D; g.ldb = H; g.ldc = H;
-  g.act = kActGelu;
+  g.act = w.pre ? kActId : kActGeluMoe;
   g.a_rows = w.perm;
   g.groups = (int)E; g.seg = w.seg; g.tiles = w.tiles; g.ntiles = w.ntiles; g.sBg = D * H;
-  if (launch_gemm_ex(g, false, false, 1, s) != 0) return -1;
+  if (w.pre) {  // training keeps the pre-activation for the backward pass
+    g.C = w.pre;
+    if (launch_gemm_ex(g, false, false, 1, s) != 0) return -1;
+    hipLaunchKernelGGL(gelu_rows_kernel, dim3((unsigned)ceil_div(M * H, 256)), dim3(256), 0, s, w.pre, w.hidden,
+                       w.seg + E, H);
+    NSH_LAUNCHED();
+  } else if (launch_gemm_ex(g, false, false, 1, s) != 0) {
+    return -1;
+  }
   // out[perm[pos]] = p[perm[pos]] * (hidden[pos] . We2[e])
   GemmArgs g2 = g;
   g2.A = w.hidden; g2.B = We2; g2.C = out;
@@ -237,6 +253,151 @@ int launch_moe_experts(const float* x, const float* We1, const float* We2, const
   hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)ceil_div(M * D, 256)), dim3(256), 0, s, w.best, out, (int)M,
                      (int)D);
   NSH_LAUNCHED();
+  return 0;
+}
+
+
+// ============================================================================
+// Backward (MOE_GRAD_X / _WG / _WE1 / _WE2, codegen.cpp:1388-1579), from the
+// forward's routing and expert-sorted rows:
+//   dpre2 = dout We2[b]^T;  dpb = sum_a gelu(u_a) dpre2_a;  sd = dpb p_b
+//   dH = dpre2 p_b gelu'(u);  dg_e = p_e ((e == b ? dpb : 0) - sd)
+//   dx = dg Wg^T + dH We1[b]^T;  dWg = x^T dg
+//   dWe1[e] = sum over e's tokens of x^T dH;  dWe2[e] = sum of (gelu(u) p_b)^T dout
+// Every product is an fp32-MFMA GEMM: grouped by expert over the sorted rows
+// (dpre2, the expert part of dx), or grouped over each expert's token
+// segment as the contraction (dWe1, dWe2).
+// ============================================================================
+
+// One wave per routed (expert-sorted) row.
+template <int EPT>
+__global__ __launch_bounds__(256) void moe_bwd_rows_kernel(const float* __restrict__ pre, const float* __restrict__ dpre2,
+                                                           const float* __restrict__ logits,
+                                                           const uint8_t* __restrict__ active,
+                                                           const int* __restrict__ perm, const int* __restrict__ best,
+                                                           const int* __restrict__ nrows, float* __restrict__ dH,
+                                                           float* __restrict__ hp, float* __restrict__ dg, int H, int E) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pos = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pos >= *nrows) return;
+  const int tok = perm[pos];
+  const int b = best[tok];
+  const float* l = logits + (int64_t)tok * E;
+  // routing probabilities, as in the forward (sequential over experts)
+  float mx = -1.0e30f, sum = 0.f;
+  if (lane == 0) {
+    for (int e = 0; e < E; e++)
+      if ((!active || active[e]) && l[e] > mx) mx = l[e];
+    for (int e = 0; e < E; e++)
+      if (!active || active[e]) sum = sum + exp_rn(l[e] - mx);
+  }
+  mx = __shfl(mx, 0, 64);
+  sum = __shfl(sum, 0, 64);
+  float pe[EPT];
+  float pb = 0.f;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = lane + 64 * j;
+    const bool live = e < E && (!active || active[e]);
+    pe[j] = (live && sum > 0.f) ? exp_rn(l[e] - mx) / sum : 0.f;
+    if (e == b) pb = pe[j];
+  }
+  pb = wave_sum(pb);  // exactly one lane holds it
+  const float* u = pre + pos * H;
+  const float* d2 = dpre2 + pos * H;
+  float* dh = dH + pos * H;
+  float* h2 = hp + pos * H;
+  float dpb = 0.f;
+  for (int a = lane; a < H; a += 64) {
+    const float ua = u[a];
+    const float ga = act_apply(ua, kActGeluMoe);
+    const float gd = act_deriv(ua, kActGeluMoe);
+    dpb += ga * d2[a];
+    dh[a] = d2[a] * pb * gd;
+    h2[a] = ga * pb;
+  }
+  dpb = wave_sum(dpb);
+  const float sd = dpb * pb;
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int e = lane + 64 * j;
+    if (e < E) dg[(int64_t)tok * E + e] = pe[j] * ((e == b ? dpb : 0.f) - sd);
+  }
+}
+
+__global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ perm,
+                                   const int* __restrict__ nrows, float* __restrict__ dst, int64_t D) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)(*nrows) * D) return;
+  dst[i] = src[(int64_t)perm[i / D] * D + i % D];
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+int launch_moe_backward(const float* x, const float* dout, const float* Wg, const float* We1, const float* We2,
+                        const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
+                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s) {
+  if (M <= 0) return 0;
+  const int* nrows = w.seg + E;
+  // dpre2[pos] = dout[perm[pos]] . We2[e]^T
+  GemmArgs g;
+  g.A = dout; g.B = We2; g.C = b.dpre2;
+  g.M = (int)M; g.N = (int)H; g.K = (int)D;
+  g.lda = D; g.ldb = D; g.ldc = H;
+  g.a_rows = w.perm;
+  g.groups = (int)E; g.seg = w.seg; g.tiles = w.tiles; g.ntiles = w.ntiles; g.sBg = H * D;
+  if (launch_gemm_ex(g, false, true, 1, s) != 0) return -1;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)ceil_div(M * E, 256)), dim3(256), 0, s, b.dg, M * E);
+  NSH_LAUNCHED();
+  const dim3 rg((unsigned)ceil_div(M, 4));
+  if (E <= 64)
+    hipLaunchKernelGGL(moe_bwd_rows_kernel<1>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
+                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
+  else if (E <= 128)
+    hipLaunchKernelGGL(moe_bwd_rows_kernel<2>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
+                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
+  else
+    hipLaunchKernelGGL(moe_bwd_rows_kernel<4>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
+                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
+  NSH_LAUNCHED();
+  // dx = dg Wg^T, then += dH We1[e]^T scattered back to token order
+  if (dx) {
+    if (launch_gemm(b.dg, Wg, dx, M, D, E, E, E, D, false, true, 0, s) != 0) return -1;
+    GemmArgs h;
+    h.A = b.dH; h.B = We1; h.C = dx;
+    h.M = (int)M; h.N = (int)D; h.K = (int)H;
+    h.lda = H; h.ldb = H; h.ldc = D;
+    h.c_rows = w.perm;
+    h.mode = kEpiAccum;
+    h.groups = (int)E; h.seg = w.seg; h.tiles = w.tiles; h.ntiles = w.ntiles; h.sBg = D * H;
+    if (launch_gemm_ex(h, false, true, 1, s) != 0) return -1;
+  }
+  // dWg = x^T dg
+  if (dWg && launch_gemm(x, b.dg, dWg, D, E, M, D, E, E, true, false, 0, s) != 0) return -1;
+  // expert-sorted copies of x and dout for the K-grouped products
+  const dim3 gd((unsigned)ceil_div(M * D, 256));
+  hipLaunchKernelGGL(gather_rows_kernel, gd, dim3(256), 0, s, x, w.perm, nrows, b.xs, D);
+  hipLaunchKernelGGL(gather_rows_kernel, gd, dim3(256), 0, s, dout, w.perm, nrows, b.ds, D);
+  NSH_LAUNCHED();
+  if (dWe1) {  // dWe1[e] [D, H] = xs[seg e]^T dH[seg e]
+    GemmArgs k;
+    k.A = b.xs; k.B = b.dH; k.C = dWe1;
+    k.M = (int)D; k.N = (int)H; k.K = (int)M;
+    k.lda = D; k.ldb = H; k.ldc = H;
+    k.kseg = w.seg; k.sC = D * H;
+    if (launch_gemm_ex(k, true, false, (int)E, s) != 0) return -1;
+  }
+  if (dWe2) {  // dWe2[e] [H, D] = hp[seg e]^T ds[seg e]
+    GemmArgs k;
+    k.A = b.hp; k.B = b.ds; k.C = dWe2;
+    k.M = (int)H; k.N = (int)D; k.K = (int)M;
+    k.lda = H; k.ldb = D; k.ldc = D;
+    k.kseg = w.seg; k.sC = H * D;
+    if (launch_gemm_ex(k, true, false, (int)E, s) != 0) return -1;
+  }
   return 0;
 }
 

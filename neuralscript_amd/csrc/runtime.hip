@@ -62,6 +62,15 @@ struct ns_model {
   std::mt19937 rng{0x9E3779B9u};  // codegen.cpp:2421
   int64_t lr_step = 0;
   int64_t moe_last_m = 0;         // tokens routed by the last MoE forward
+  struct Adam {
+    float* m = nullptr;
+    float* v = nullptr;
+    int64_t t = 0;
+  };
+  std::map<int, Adam> adam;       // AdamW state per weight value id
+  std::vector<MuonMat> muon_host; // descriptors of the last optimizer step
+  std::vector<float*> last_ptr;   // value buffers of the last call (read-back)
+  std::vector<size_t> last_numel;
   std::vector<Buf> arena;         // per value id
   std::map<std::string, Buf> scratch;
   // profiling
@@ -177,6 +186,7 @@ int moe_work(ns_model* m, int64_t M, MoeWork* w) {
   w->seg = w->bcount + nblk * q.E;
   w->tiles = w->seg + q.E + 1;
   w->ntiles = w->tiles + 2 * (ceil_div(M, 128) + q.E + 1);
+  w->pre = nullptr;
   return 0;
 }
 
@@ -190,6 +200,11 @@ int bind_weights(ns_model* m, Frame& fr) {
     fr.ptr[id] = m->d_w + v.offset;
   }
   return 0;
+}
+
+void keep_frame(ns_model* m, const Frame& fr) {
+  m->last_ptr = fr.ptr;
+  m->last_numel = fr.numel;
 }
 
 float* out_buf(ns_model* m, Frame& fr, int id, size_t n) {
@@ -297,6 +312,7 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       NSH_OUT(out, I.res, (size_t)(M * q.D));
       MoeWork w;
       if (moe_work(m, M, &w) != 0) return -1;
+      if (train && !(w.pre = scratch(m, "moe_pre", (size_t)(M * q.H)))) return -1;
       Prof p(m, "moe");
       if (launch_moe_route(fr.ptr[I.in[0]], fr.ptr[I.in[1]], m->d_active, w, M, q.D, q.E, s) != 0) return -1;
       m->moe_last_m = M;
@@ -329,12 +345,365 @@ int run_forward(ns_model* m, const float* d_x, size_t n_in, float** d_out, size_
     if (I.fused_away || I.op == Op::Marker) continue;
     if (exec_forward_op(m, F, I, fr, false) != 0) return -1;
   }
+  keep_frame(m, fr);
   if (F.ret < 0) {
     set_error("forward function has no return value");
     return -1;
   }
   *d_out = fr.ptr[F.ret];
   *n_out = fr.numel[F.ret];
+  return 0;
+}
+
+
+// ---------------------------------------------------------------------------
+// Training: forward body, reverse body, optimizer body (emit_train_core,
+// codegen.cpp:2755-3157), with these fusions:
+//  * CROSS_ENTROPY computes the LOSS_GRAD seed of the same logits in the same
+//    pass (one read of logits and labels);
+//  * MATMUL_GRAD_A whose only consumer is an ACTIVATION_GRAD applies act'(pre)
+//    in the GEMM epilogue;
+//  * the five ATTENTION_GRAD_* of one layer come from one backward pass (the
+//    reference recomputes the layer for each; the recomputation is
+//    deterministic, so one pass yields the same five quantities).
+// ---------------------------------------------------------------------------
+int uses_of(const Func& F, int id) {
+  int u = 0;
+  for (auto& J : F.ins)
+    for (int v : J.in) u += v == id;
+  return u;
+}
+
+struct AttnGrads {
+  float* dX = nullptr;
+  float* dW3 = nullptr;  // [3][D][D] dWq, dWk, dWv
+  float* dWo = nullptr;
+};
+
+int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
+  const Plan& P = *m->plan;
+  hipStream_t s = m->stream;
+  const int x = I.in[1];
+  auto it = fr.attn.find(x);
+  if (it == fr.attn.end()) {
+    set_error("attention backward without its forward");
+    return -1;
+  }
+  const AttnSaved& sv = it->second;
+  const int64_t D = P.vals[I.in[2]].rows, H = I.heads, BS = sv.BS;
+  const std::string key = std::to_string(x);
+  float* dPre = scratch(m, "ag_dpre" + key, (size_t)(BS * D));
+  float* dqkv = scratch(m, "ag_dqkv" + key, (size_t)(3 * BS * D));
+  float* delta = scratch(m, "ag_delta" + key, (size_t)(H * BS));
+  out->dX = scratch(m, "ag_dx" + key, (size_t)(BS * D));
+  out->dW3 = scratch(m, "ag_dw3" + key, (size_t)(3 * D * D));
+  out->dWo = scratch(m, "ag_dwo" + key, (size_t)(D * D));
+  if (!dPre || !dqkv || !delta || !out->dX || !out->dW3 || !out->dWo) return -1;
+  const float* dout = fr.ptr[I.in[0]];
+  const float* xin = fr.ptr[x];
+  const float* Wq = fr.ptr[I.in[2]];
+  const float* Wk = fr.ptr[I.in[3]];
+  const float* Wv = fr.ptr[I.in[4]];
+  const float* Wo = fr.ptr[I.in[5]];
+  if (BS == 0) return 0;
+  {
+    Prof p(m, "gemm");
+    // dPre = dout Wo^T
+    if (launch_gemm(dout, Wo, dPre, BS, D, D, D, D, D, false, true, 0, s) != 0) return -1;
+    // dWo = ctx^T dout
+    if (launch_gemm(sv.ctx, dout, out->dWo, D, D, BS, D, D, D, true, false, 0, s) != 0) return -1;
+  }
+  {
+    Prof p(m, "attention_bwd");
+    if (launch_attention_bwd(sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, dPre, sv.lse, delta, dqkv,
+                             dqkv + BS * D, dqkv + 2 * BS * D, BS, D, H, D, s) != 0)
+      return -1;
+  }
+  Prof p(m, "gemm");
+  // dWq, dWk, dWv = x^T [dQ | dK | dV]  (one batched launch)
+  GemmArgs g;
+  g.A = xin; g.B = dqkv; g.C = out->dW3;
+  g.M = (int)D; g.N = (int)D; g.K = (int)BS;
+  g.lda = D; g.ldb = D; g.ldc = D;
+  g.sA = 0; g.sB = BS * D; g.sC = D * D;
+  if (launch_gemm_ex(g, true, false, 3, s) != 0) return -1;
+  // dX = dQ Wq^T + dK Wk^T + dV Wv^T
+  const float* Ws[3] = {Wq, Wk, Wv};
+  for (int j = 0; j < 3; j++) {
+    GemmArgs h;
+    h.A = dqkv + j * BS * D; h.B = Ws[j]; h.C = out->dX;
+    h.M = (int)BS; h.N = (int)D; h.K = (int)D;
+    h.lda = D; h.ldb = D; h.ldc = D;
+    h.mode = j == 0 ? kEpiAct : kEpiAccum;
+    if (launch_gemm_ex(h, false, true, 1, s) != 0) return -1;
+  }
+  return 0;
+}
+
+// Muon step of several matrices: descriptors to the device, gather, MGS
+// column steps, update.
+int muon_batch(MuonMat* d, const std::vector<MuonMat>& mats, int64_t max_elems, int max_c, int total_blocks,
+               hipStream_t s) {
+  const int nm = (int)mats.size();
+  NSH_CHECK(hipMemcpyAsync(d, mats.data(), nm * sizeof(MuonMat), hipMemcpyHostToDevice, s));
+  if (launch_muon_gather(d, nm, max_elems, s) != 0) return -1;
+  if (launch_mgs_steps(d, nm, total_blocks, max_c, s) != 0) return -1;
+  return launch_muon_update(d, nm, max_elems, s);
+}
+
+int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
+  const Plan& P = *m->plan;
+  hipStream_t s = m->stream;
+  m->muon_host.clear();
+  int64_t max_elems = 0;
+  int max_c = 0, total_blocks = 0;
+  for (size_t k = 0; k + 1 < I.in.size(); k += 2) {
+    const int wid = I.in[k], gid = I.in[k + 1];
+    const Value& W = P.vals[wid];
+    const int64_t r = W.rows, c = W.cols, n = r * c;
+    float* w = fr.ptr[wid];
+    const float* g = fr.ptr[gid];
+    if (!g || fr.numel[gid] < (size_t)n) {
+      set_error("optimizer: missing gradient for " + W.name);
+      return -1;
+    }
+    const bool muon = r > 1 && c > 1 && std::min(r, c) >= 8;  // codegen.cpp:3097
+    if (muon) {
+      MuonMat mm;
+      mm.w = w;
+      mm.g = g;
+      mm.transposed = r < c ? 1 : 0;
+      mm.R = (int)(r < c ? c : r);
+      mm.C = (int)(r < c ? r : c);
+      mm.T = scratch(m, "muonT" + std::to_string(wid), (size_t)n);
+      mm.norms = scratch(m, "muonN" + std::to_string(wid), (size_t)mm.C);
+      if (!mm.T || !mm.norms) return -1;
+      mm.nblk = muon_blocks(mm.C);
+      mm.le = lr * sqrtf((float)std::min(r, c));
+      mm.decay = 0.01f * lr;
+      m->muon_host.push_back(mm);
+      max_elems = std::max(max_elems, n);
+      max_c = std::max(max_c, mm.C);
+      total_blocks += mm.nblk;
+    } else {
+      auto& st = m->adam[wid];
+      if (!st.m) {
+        NSH_CHECK(hipMalloc(&st.m, (size_t)n * sizeof(float)));
+        NSH_CHECK(hipMalloc(&st.v, (size_t)n * sizeof(float)));
+        NSH_CHECK(hipMemsetAsync(st.m, 0, (size_t)n * sizeof(float), s));
+        NSH_CHECK(hipMemsetAsync(st.v, 0, (size_t)n * sizeof(float), s));
+      }
+      st.t += 1;
+      const float b1t = 1.f - powf(0.9f, (float)st.t), b2t = 1.f - powf(0.999f, (float)st.t);
+      Prof p(m, "adamw");
+      if (launch_adamw(w, g, st.m, st.v, n, lr, b1t, b2t, s) != 0) return -1;
+    }
+  }
+  if (m->muon_host.empty()) return 0;
+  const int nm = (int)m->muon_host.size();
+  MuonMat* d = reinterpret_cast<MuonMat*>(scratch(m, "muon_desc", (nm * sizeof(MuonMat) + 3) / 4));
+  if (!d) return -1;
+  Prof p(m, "muon");
+  return muon_batch(d, m->muon_host, max_elems, max_c, total_blocks, s);
+}
+
+int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, float lr, bool train_mode,
+              float** d_loss) {
+  const Plan& P = *m->plan;
+  const Func& F = P.trn;
+  hipStream_t s = m->stream;
+  Frame fr;
+  bind_weights(m, fr);
+  fr.numel[F.x] = n_in;
+  fr.ptr[F.x] = const_cast<float*>(d_x);
+  float* loss = scratch(m, "loss", 1);
+  if (!loss) return -1;
+  *d_loss = loss;
+  std::map<int, AttnGrads> agrads;
+  bool moe_done = false;
+  float *moe_dx = nullptr, *moe_dwg = nullptr, *moe_dwe1 = nullptr, *moe_dwe2 = nullptr;
+  std::vector<bool> skip(F.ins.size(), false);
+  for (size_t ii = 0; ii < F.ins.size(); ii++) {
+    const Instr& I = F.ins[ii];
+    if (skip[ii] || I.op == Op::Marker) continue;
+    switch (I.op) {
+      case Op::Matmul: case Op::Act: case Op::Embedding: case Op::LayerNorm: case Op::Attention: case Op::Moe:
+      case Op::Dropout:
+        if (exec_forward_op(m, F, I, fr, true) != 0) return -1;
+        break;
+      case Op::CrossEntropy: {
+        // C = the logits' columns (codegen.cpp:2901-2906), rows = numel / C
+        int64_t C = F.width[I.in[0]] > 0 ? F.width[I.in[0]] : P.in_cols;
+        const size_t n = fr.numel[I.in[0]];
+        const int64_t rows = (int64_t)(n / (size_t)C);
+        fr.numel[F.y] = n;
+        fr.ptr[F.y] = const_cast<float*>(d_y);
+        float* rl = scratch(m, "row_loss", (size_t)std::max<int64_t>(rows, 1));
+        if (!rl) return -1;
+        float* grad = nullptr;
+        if (train_mode) {
+          for (size_t jj = ii + 1; jj < F.ins.size(); jj++) {
+            const Instr& J = F.ins[jj];
+            if (J.op == Op::LossGrad && J.in[0] == I.in[0] && J.in[1] == I.in[1]) {
+              grad = out_buf(m, fr, J.res, n);
+              if (!grad) return -1;
+              skip[jj] = true;
+              break;
+            }
+          }
+        }
+        Prof p(m, "softmax_xent");
+        if (launch_softmax_xent(fr.ptr[I.in[0]], d_y, grad, rl, loss, rows, C, grad != nullptr, s) != 0) return -1;
+        break;
+      }
+      default:
+        if (!train_mode) break;
+        switch (I.op) {
+          case Op::LossGrad: {
+            const int64_t C = F.width[I.in[0]] > 0 ? F.width[I.in[0]] : P.in_cols;
+            const size_t n = fr.numel[I.in[0]];
+            const int64_t rows = (int64_t)(n / (size_t)C);
+            NSH_OUT(grad, I.res, n);
+            float* rl = scratch(m, "row_loss", (size_t)std::max<int64_t>(rows, 1));
+            float* tmp = scratch(m, "loss_tmp", 1);
+            if (!rl || !tmp) return -1;
+            Prof p(m, "softmax_xent");
+            if (launch_softmax_xent(fr.ptr[I.in[0]], d_y, grad, rl, tmp, rows, C, true, s) != 0) return -1;
+            break;
+          }
+          case Op::MatmulGradA: {
+            const Value& B = P.vals[I.in[1]];
+            const int64_t K = B.rows, N = B.cols;
+            const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)N);
+            GemmArgs g;
+            g.A = fr.ptr[I.in[0]]; g.B = fr.ptr[I.in[1]];
+            g.M = (int)M; g.N = (int)K; g.K = (int)N;
+            g.lda = N; g.ldb = N; g.ldc = K;
+            int res = I.res;
+            if (ii + 1 < F.ins.size()) {
+              const Instr& J = F.ins[ii + 1];
+              if (J.op == Op::ActGrad && J.in[0] == I.res && uses_of(F, I.res) == 1) {
+                g.mode = kEpiActGrad;
+                g.act = J.act;
+                g.aux = fr.ptr[J.in[1]];
+                g.ldaux = K;
+                res = J.res;
+                skip[ii + 1] = true;
+              }
+            }
+            NSH_OUT(C, res, (size_t)(M * K));
+            g.C = C;
+            Prof p(m, "gemm");
+            if (launch_gemm_ex(g, false, true, 1, s) != 0) return -1;
+            break;
+          }
+          case Op::MatmulGradW: {
+            const Value& B = P.vals[I.in[2]];
+            const int64_t K = B.rows, N = B.cols;
+            const int64_t M = (int64_t)(fr.numel[I.in[1]] / (size_t)N);
+            NSH_OUT(C, I.res, (size_t)(K * N));
+            Prof p(m, "gemm");
+            if (launch_gemm(fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, K, N, M, K, N, N, true, false, 0, s) != 0) return -1;
+            break;
+          }
+          case Op::ActGrad: {
+            const size_t n = fr.numel[I.in[0]];
+            NSH_OUT(y, I.res, n);
+            Prof p(m, "act_grad");
+            if (launch_act_grad(fr.ptr[I.in[0]], fr.ptr[I.in[1]], y, (int64_t)n, I.act, s) != 0) return -1;
+            break;
+          }
+          case Op::LayerNormGrad: {
+            int64_t last = F.width[I.in[1]];
+            if (last <= 0) last = 1;
+            const size_t n = fr.numel[I.in[0]];
+            NSH_OUT(y, I.res, n);
+            Prof p(m, "layernorm_grad");
+            if (launch_layernorm_grad(fr.ptr[I.in[0]], fr.ptr[I.in[1]], y, (int64_t)(n / (size_t)last), last, s) != 0)
+              return -1;
+            break;
+          }
+          case Op::EmbeddingGradW: {
+            const Value& W = P.vals[I.in[2]];
+            const int64_t n = (int64_t)(fr.numel[I.in[0]] / (size_t)W.cols);
+            NSH_OUT(dW, I.res, (size_t)(W.rows * W.cols));
+            int* ws = reinterpret_cast<int*>(scratch(m, "emb_ws", embedding_grad_workspace(n, W.rows)));
+            if (!ws) return -1;
+            Prof p(m, "embedding_grad");
+            if (launch_embedding_grad(fr.ptr[I.in[0]], fr.ptr[I.in[1]], dW, n, W.rows, W.cols, ws, s) != 0)
+              return -1;
+            break;
+          }
+          case Op::AttnGradX: case Op::AttnGradWq: case Op::AttnGradWk: case Op::AttnGradWv: case Op::AttnGradWo: {
+            const int x = I.in[1];
+            if (!agrads.count(x)) {
+              AttnGrads ag;
+              if (attention_backward(m, fr, I, &ag) != 0) return -1;
+              agrads[x] = ag;
+            }
+            const AttnGrads& ag = agrads[x];
+            const int64_t D = P.vals[I.in[2]].rows;
+            const size_t dd = (size_t)(D * D);
+            float* p = nullptr;
+            size_t n = dd;
+            switch (I.op) {
+              case Op::AttnGradX: p = ag.dX; n = fr.numel[I.in[0]]; break;
+              case Op::AttnGradWq: p = ag.dW3; break;
+              case Op::AttnGradWk: p = ag.dW3 + dd; break;
+              case Op::AttnGradWv: p = ag.dW3 + 2 * dd; break;
+              default: p = ag.dWo; break;
+            }
+            fr.ptr[I.res] = p;
+            fr.numel[I.res] = n;
+            break;
+          }
+          case Op::MoeGradX: case Op::MoeGradWg: case Op::MoeGradWe1: case Op::MoeGradWe2: {
+            const MoeInfo& q = P.moe;
+            const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)q.D);
+            if (!moe_done) {
+              MoeWork w;
+              if (moe_work(m, M, &w) != 0) return -1;
+              w.pre = scratch(m, "moe_pre", (size_t)(M * q.H));
+              MoeBwdWork b;
+              b.dpre2 = scratch(m, "moe_dpre2", (size_t)(M * q.H));
+              b.dH = scratch(m, "moe_dH", (size_t)(M * q.H));
+              b.hp = scratch(m, "moe_hp", (size_t)(M * q.H));
+              b.dg = scratch(m, "moe_dg", (size_t)(M * q.E));
+              b.xs = scratch(m, "moe_xs", (size_t)(M * q.D));
+              b.ds = scratch(m, "moe_ds", (size_t)(M * q.D));
+              moe_dx = scratch(m, "moe_gx", (size_t)(M * q.D));
+              moe_dwg = scratch(m, "moe_gwg", (size_t)(q.D * q.E));
+              moe_dwe1 = scratch(m, "moe_gwe1", (size_t)(q.E * q.D * q.H));
+              moe_dwe2 = scratch(m, "moe_gwe2", (size_t)(q.E * q.H * q.D));
+              if (!w.pre || !b.dpre2 || !b.dH || !b.hp || !b.dg || !b.xs || !b.ds || !moe_dx || !moe_dwg ||
+                  !moe_dwe1 || !moe_dwe2)
+                return -1;
+              Prof p(m, "moe_bwd");
+              if (launch_moe_backward(fr.ptr[I.in[1]], fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]],
+                                      fr.ptr[I.in[4]], m->d_active, w, b, moe_dx, moe_dwg, moe_dwe1, moe_dwe2, M, q.D,
+                                      q.H, q.E, s) != 0)
+                return -1;
+              moe_done = true;
+            }
+            switch (I.op) {
+              case Op::MoeGradX: fr.ptr[I.res] = moe_dx; fr.numel[I.res] = (size_t)(M * q.D); break;
+              case Op::MoeGradWg: fr.ptr[I.res] = moe_dwg; fr.numel[I.res] = (size_t)(q.D * q.E); break;
+              case Op::MoeGradWe1: fr.ptr[I.res] = moe_dwe1; fr.numel[I.res] = (size_t)(q.E * q.D * q.H); break;
+              default: fr.ptr[I.res] = moe_dwe2; fr.numel[I.res] = (size_t)(q.E * q.H * q.D); break;
+            }
+            break;
+          }
+          case Op::OptStep:
+            if (optimizer_step(m, fr, I, lr) != 0) return -1;
+            m->host_stale = true;
+            break;
+          default:
+            set_error("training instruction not supported by this build of libnship");
+            return -1;
+        }
+    }
+  }
+  keep_frame(m, fr);
   return 0;
 }
 
@@ -476,6 +845,10 @@ void nsh_model_free(ns_model* m) {
   for (auto e : m->event_pool) hipEventDestroy(e);
   if (m->d_w) hipFree(m->d_w);
   if (m->d_active) hipFree(m->d_active);
+  for (auto& kv : m->adam) {
+    if (kv.second.m) hipFree(kv.second.m);
+    if (kv.second.v) hipFree(kv.second.v);
+  }
   if (m->stream) hipStreamDestroy(m->stream);
   delete m;
 }
@@ -652,18 +1025,78 @@ size_t nsh_expert_kill(ns_model* m, int k) {
   return m->moe_count;
 }
 
-int nsh_train_step(ns_model* m, const float* input, const float* labels, size_t input_numel,
-                   float* loss_out, float lr) {
-  (void)m; (void)input; (void)labels; (void)input_numel; (void)loss_out; (void)lr;
-  set_error("training is not available in this build");
-  return -1;
+// Host-pointer training step: the wrapper of codegen.cpp:2636-2644 (LR
+// schedule step counter; the compiled-in schedule is constant, multiplier 1).
+int nsh_train_step_device(ns_model* m, const float* d_input, const float* d_labels, size_t input_numel,
+                          float* loss_out, float lr) {
+  if (!m || !d_input || !d_labels) {
+    set_error("train: null argument");
+    return -1;
+  }
+  if (!m->plan->has_train) {
+    set_error("train: the network has no train() method");
+    return -1;
+  }
+  const int64_t st = m->lr_step;
+  if (st < INT64_MAX) m->lr_step = st + 1;
+  const float lr_eff = lr * 1.0f;
+  float* d_loss = nullptr;
+  if (run_train(m, d_input, input_numel, d_labels, lr_eff, true, &d_loss) != 0) return -1;
+  if (loss_out) {
+    NSH_CHECK(hipMemcpyAsync(loss_out, d_loss, sizeof(float), hipMemcpyDeviceToHost, m->stream));
+    return sync(m);
+  }
+  return 0;
+}
+
+static int stage_train_inputs(ns_model* m, const float* input, const float* labels, size_t input_numel,
+                              float** dx, float** dy) {
+  const Plan& P = *m->plan;
+  const size_t rows = (size_t)((int64_t)input_numel / P.in_cols);
+  const size_t ny = rows * (size_t)P.out_cols;
+  Buf& xb = m->scratch["__x"];
+  Buf& yb = m->scratch["__y"];
+  if (ensure(xb, input_numel) != 0 || ensure(yb, ny) != 0) return -1;
+  NSH_CHECK(hipMemcpyAsync(xb.p, input, input_numel * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  NSH_CHECK(hipMemcpyAsync(yb.p, labels, ny * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  *dx = xb.p;
+  *dy = yb.p;
+  return 0;
+}
+
+int nsh_train_step(ns_model* m, const float* input, const float* labels, size_t input_numel, float* loss_out,
+                   float lr) {
+  if (!m || !input || !labels) {
+    set_error("train: null argument");
+    return -1;
+  }
+  float *dx = nullptr, *dy = nullptr;
+  if (stage_train_inputs(m, input, labels, input_numel, &dx, &dy) != 0) return -1;
+  float loss = 0.f;
+  if (nsh_train_step_device(m, dx, dy, input_numel, &loss, lr) != 0) return -1;
+  if (loss_out) *loss_out = loss;
+  return 0;
 }
 
 int nsh_objective_loss(ns_model* m, const float* input, const float* labels, size_t input_numel,
                        float* loss_out) {
-  (void)m; (void)input; (void)labels; (void)input_numel; (void)loss_out;
-  set_error("training is not available in this build");
-  return -1;
+  if (!m || !input || !labels) {
+    set_error("objective: null argument");
+    return -1;
+  }
+  if (!m->plan->has_train) {
+    set_error("objective: the network has no train() method");
+    return -1;
+  }
+  float *dx = nullptr, *dy = nullptr;
+  if (stage_train_inputs(m, input, labels, input_numel, &dx, &dy) != 0) return -1;
+  float* d_loss = nullptr;
+  if (run_train(m, dx, input_numel, dy, 0.f, false, &d_loss) != 0) return -1;
+  float loss = 0.f;
+  NSH_CHECK(hipMemcpyAsync(&loss, d_loss, sizeof(float), hipMemcpyDeviceToHost, m->stream));
+  if (sync(m) != 0) return -1;
+  if (loss_out) *loss_out = loss;
+  return 0;
 }
 
 // ---- profiling ---------------------------------------------------------------
@@ -696,6 +1129,34 @@ int nsh_profile_report(ns_model* m, char* buf, size_t len) {
   s += "}";
   if (s.size() + 1 > len) return -1;
   std::memcpy(buf, s.c_str(), s.size() + 1);
+  return 0;
+}
+
+// Contents of IR value `name` as left by the last forward / training call
+// (weights: their current values).  n must equal the value's element count.
+int nsh_model_read_value(ns_model* m, const char* name, float* out, size_t n) {
+  if (!m || !name || !out) return -1;
+  auto it = m->plan->index.find(name);
+  if (it == m->plan->index.end()) {
+    set_error(std::string("read_value: no value named ") + name);
+    return -1;
+  }
+  const int id = it->second;
+  if (sync(m) != 0) return -1;
+  const float* p = nullptr;
+  size_t cnt = 0;
+  if (m->plan->vals[id].weight) {
+    p = m->d_w + m->plan->vals[id].offset;
+    cnt = (size_t)(m->plan->vals[id].rows * m->plan->vals[id].cols);
+  } else if ((size_t)id < m->last_ptr.size()) {
+    p = m->last_ptr[id];
+    cnt = m->last_numel[id];
+  }
+  if (!p || cnt != n) {
+    set_error(std::string("read_value: ") + name + " not available with that size");
+    return -1;
+  }
+  NSH_CHECK(hipMemcpy(out, p, n * sizeof(float), hipMemcpyDeviceToHost));
   return 0;
 }
 
@@ -763,6 +1224,95 @@ size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V) { return embedding_
 int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                           void* workspace) {
   if (!workspace || launch_embedding_grad(dout, idx, dW, n, V, D, (int*)workspace, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+// One Muon matrix on device buffers: w -= lr sqrt(min(r,c)) MGS(g) + 0.01 lr w.
+// With w zeroed, lr = -1 and decay 0 it returns MGS(g) itself (orthonormalize).
+static int op_muon(float* w, const float* g, int64_t r, int64_t c, float le, float decay, void* ws) {
+  if (!w || !g || !ws || r <= 0 || c <= 0) {
+    set_error("muon: bad arguments");
+    return -1;
+  }
+  MuonMat mm;
+  mm.w = w;
+  mm.g = g;
+  mm.transposed = r < c ? 1 : 0;
+  mm.R = (int)(r < c ? c : r);
+  mm.C = (int)(r < c ? r : c);
+  char* base = (char*)ws;
+  mm.T = (float*)(base + 256);
+  mm.norms = mm.T + r * c;
+  mm.nblk = muon_blocks(mm.C);
+  mm.le = le;
+  mm.decay = decay;
+  MuonMat* d = (MuonMat*)base;
+  NSH_CHECK(hipMemcpy(d, &mm, sizeof(mm), hipMemcpyHostToDevice));
+  if (launch_muon_gather(d, 1, r * c, nullptr) != 0) return -1;
+  if (launch_mgs_steps(d, 1, mm.nblk, mm.C, nullptr) != 0) return -1;
+  if (launch_muon_update(d, 1, r * c, nullptr) != 0) return -1;
+  NSH_CHECK(hipStreamSynchronize(nullptr));
+  return 0;
+}
+
+int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64_t* r, const int64_t* c, float lr,
+                      void* workspace) {
+  if (n <= 0 || !w || !g || !r || !c || !workspace) {
+    set_error("muon_multi: bad arguments");
+    return -1;
+  }
+  std::vector<MuonMat> mats;
+  char* base = (char*)workspace;
+  MuonMat* d = (MuonMat*)base;
+  float* wsf = (float*)(base + 256 * (((size_t)n * sizeof(MuonMat) + 255) / 256));
+  int64_t max_elems = 0;
+  int max_c = 0, total = 0;
+  for (int i = 0; i < n; i++) {
+    MuonMat mm;
+    mm.w = w[i];
+    mm.g = g[i];
+    mm.transposed = r[i] < c[i] ? 1 : 0;
+    mm.R = (int)(r[i] < c[i] ? c[i] : r[i]);
+    mm.C = (int)(r[i] < c[i] ? r[i] : c[i]);
+    mm.T = wsf;
+    wsf += r[i] * c[i];
+    mm.norms = wsf;
+    wsf += mm.C;
+    mm.nblk = muon_blocks(mm.C);
+    mm.le = lr * sqrtf((float)std::min(r[i], c[i]));
+    mm.decay = 0.01f * lr;
+    mats.push_back(mm);
+    max_elems = std::max(max_elems, r[i] * c[i]);
+    max_c = std::max(max_c, mm.C);
+    total += mm.nblk;
+  }
+  if (muon_batch(d, mats, max_elems, max_c, total, nullptr) != 0) return -1;
+  NSH_CHECK(hipStreamSynchronize(nullptr));
+  return 0;
+}
+
+size_t nsh_op_muon_multi_workspace(int n, const int64_t* r, const int64_t* c) {
+  size_t b = 256 * (((size_t)n * sizeof(MuonMat) + 255) / 256);
+  for (int i = 0; i < n; i++) b += (size_t)(r[i] * c[i] + std::min(r[i], c[i])) * sizeof(float);
+  return b;
+}
+
+size_t nsh_op_muon_workspace(int64_t r, int64_t c) {
+  return 256 + (size_t)(r * c + std::min(r, c)) * sizeof(float);
+}
+
+int nsh_op_orthonormalize(const float* g, float* q, int64_t r, int64_t c, void* workspace) {
+  NSH_CHECK(hipMemset(q, 0, (size_t)(r * c) * sizeof(float)));
+  return op_muon(q, g, r, c, -1.0f, 0.0f, workspace);
+}
+
+int nsh_op_muon_step(float* w, const float* g, int64_t r, int64_t c, float lr, void* workspace) {
+  return op_muon(w, g, r, c, lr * sqrtf((float)std::min(r, c)), 0.01f * lr, workspace);
+}
+
+int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr) {
+  const float b1t = 1.f - powf(0.9f, (float)t), b2t = 1.f - powf(0.999f, (float)t);
+  if (launch_adamw(w, g, m, v, n, lr, b1t, b2t, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 

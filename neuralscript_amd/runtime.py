@@ -71,6 +71,14 @@ def lib():
             "nsh_profile_report": (ci, [vp, ctypes.c_char_p, sz]),
             "nsh_op_gemm": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, ci]),
             "nsh_model_last_routing": (ci, [vp, vp, vp, vp, sz]),
+            "nsh_train_step_device": (ci, [vp, vp, vp, sz, _f32p, cf]),
+            "nsh_model_read_value": (ci, [vp, ctypes.c_char_p, vp, sz]),
+            "nsh_op_muon_workspace": (sz, [i64, i64]),
+            "nsh_op_orthonormalize": (ci, [vp, vp, i64, i64, vp]),
+            "nsh_op_muon_step": (ci, [vp, vp, i64, i64, cf, vp]),
+            "nsh_op_adamw_step": (ci, [vp, vp, vp, vp, i64, i64, cf]),
+            "nsh_op_muon_multi_workspace": (sz, [ci, vp, vp]),
+            "nsh_op_muon_multi": (ci, [ci, vp, vp, vp, vp, cf, vp]),
             "nsh_op_embedding": (ci, [vp, vp, vp, i64, i64, i64]),
             "nsh_op_layernorm": (ci, [vp, vp, i64, i64]),
             "nsh_op_layernorm_grad": (ci, [vp, vp, vp, i64, i64]),
@@ -218,6 +226,13 @@ class Model:
                                    loss.ctypes.data_as(_f32p), ctypes.c_float(lr)), "train_step")
         return loss[0]
 
+    def train_step_device(self, d_x: DeviceArray, d_y: DeviceArray, lr, want_loss=True):
+        loss = np.zeros(1, dtype=np.float32)
+        check(lib().nsh_train_step_device(self.h, d_x.ptr, d_y.ptr, d_x.n,
+                                          loss.ctypes.data_as(_f32p) if want_loss else None,
+                                          ctypes.c_float(lr)), "train_step_device")
+        return loss[0]
+
     def objective_loss(self, x, labels):
         x = np.ascontiguousarray(x, dtype=np.float32).ravel()
         y = np.ascontiguousarray(labels, dtype=np.float32).ravel()
@@ -225,6 +240,11 @@ class Model:
         check(lib().nsh_objective_loss(self.h, x.ctypes.data_as(_f32p), y.ctypes.data_as(_f32p), x.size,
                                        loss.ctypes.data_as(_f32p)), "objective_loss")
         return loss[0]
+
+    def read_value(self, name, n):
+        out = np.empty(n, dtype=np.float32)
+        check(lib().nsh_model_read_value(self.h, name.encode(), out.ctypes.data, n), "read_value " + name)
+        return out
 
     def last_routing(self, n, E):
         best = np.empty(n, dtype=np.int32)

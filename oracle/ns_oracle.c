@@ -814,6 +814,11 @@ EXPORT void or_moe_bwd(const float* dout, const float* x, const float* Wg, const
 /* optimizer                                                               */
 /* ---------------------------------------------------------------------- */
 
+/* Number of interleaved partial sums in the MGS dot products: 1 (default)
+ * is the reference's order; 2..8 are test-only reorderings. */
+static int g_mgs_partials = 1;
+EXPORT void or_set_mgs_partials(int p) { g_mgs_partials = (p < 1) ? 1 : (p > 8 ? 8 : p); }
+
 /* Modified Gram-Schmidt over columns (M >= N) or rows (M < N), in place;
  * ns_orthonom codegen.cpp:1617-1633.  Right-looking form: when column j is
  * final, every later column is projected against it.  Each column sees the
@@ -838,7 +843,17 @@ EXPORT void or_orthonom(float* G, int64_t M, int64_t N) {
         for (int64_t c = j + 1; c < C; c++) {
             float* v = T + (size_t)c * R;
             float dot = 0.f;
-            for (int64_t k = 0; k < R; k++) dot += q[k] * v[k];
+            if (g_mgs_partials <= 1) {
+                for (int64_t k = 0; k < R; k++) dot += q[k] * v[k];
+            } else {
+                /* Test-only: the same dot product as P interleaved partial
+                 * sums, to measure how far a mere change of summation order
+                 * moves the reference's training trajectory. */
+                float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                const int P = g_mgs_partials;
+                for (int64_t k = 0; k < R; k++) part[k % P] += q[k] * v[k];
+                for (int p = 0; p < P; p++) dot += part[p];
+            }
             for (int64_t k = 0; k < R; k++) v[k] -= dot * q[k];
         }
     }

@@ -43,6 +43,12 @@ def build_command():
             "-fopenmp", "-fPIC", "-shared", src, "-o", LIB_PATH, "-lm"]
 
 
+def set_mgs_partials(p):
+    """Test-only: sum each MGS dot product as p interleaved partial sums
+    (1 = the reference's order)."""
+    lib().or_set_mgs_partials(int(p))
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -76,6 +82,7 @@ def lib():
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, sz, i64, cf]),
             "or_use_muon": (ci, [i64, i64]),
             "or_lr_scale_cosine": (cf, [i64]),
+            "or_set_mgs_partials": (None, [ci]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

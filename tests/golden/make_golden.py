@@ -52,6 +52,16 @@ def case_inputs(name, rows, seed):
     return net, x, y
 
 
+# 100-step loss curves, host-side cosine warmup schedule (lr * lr_scale(t),
+# t = 0..99, so the first step has lr 0), on reduced c5 twins:
+# name, tokens, seed, base lr
+CURVES = [("c5s", 256, 201, 3e-4), ("c5s", 256, 202, 0.02), ("c5t", 96, 203, 0.05)]
+
+
+def curve_lrs(base, steps=100):
+    return [np.float32(base) * np.float32(oracle.lr_scale_cosine(t)) for t in range(steps)]
+
+
 def digest(a):
     return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()[:16]
 
@@ -85,5 +95,23 @@ def main():
         print(name, {k: getattr(v, "shape", None) for k, v in rec.items()})
 
 
+def curves():
+    for name, rows, seed, base in CURVES:
+        net = oracle.Net(helpers.ir_text(name))
+        x = helpers.net_inputs(net, name, seed, rows)
+        y = helpers.net_labels(net, seed, rows)
+        w = helpers.net_weights(name, seed, std=0.1)
+        lib = NsLib(os.path.join(helpers.REF, f"lib{name}.so"))
+        m = lib.init(w)
+        losses = np.array([lib.train_step(m, x, y, lr) for lr in curve_lrs(base)], dtype=np.float32)
+        wf = lib.get_weights(m)
+        lib.free(m)
+        tag = f"curve_{name}_{seed}"
+        np.savez_compressed(os.path.join(HERE, tag + ".npz"), losses=losses, x_digest=np.array(digest(x)),
+                            w_final_digest=np.array(digest(wf)))
+        print(tag, losses[[0, 1, 50, 99]])
+
+
 if __name__ == "__main__":
     main()
+    curves()

@@ -261,3 +261,21 @@ def test_lr_cosine_schedule_values():
 def test_optimizer_rule_by_shape():
     assert oracle.use_muon(8, 8) and oracle.use_muon(512, 8192)
     assert not oracle.use_muon(7, 100) and not oracle.use_muon(1, 64) and not oracle.use_muon(2, 16)
+
+
+@pytest.mark.parametrize("curve", __import__("golden.make_golden", fromlist=["CURVES"]).CURVES,
+                         ids=lambda c: f"{c[0]}-{c[2]}")
+def test_oracle_reproduces_reference_loss_curves(curve):
+    """100 training steps with the host-side cosine warmup: every loss and the
+    final weights bit-identical to the reference build's."""
+    from golden.make_golden import curve_lrs
+    name, rows, seed, base = curve
+    g = np.load(os.path.join(helpers.GOLDEN, f"curve_{name}_{seed}.npz"))
+    net = oracle.Net(helpers.ir_text(name))
+    x = helpers.net_inputs(net, name, seed, rows)
+    y = helpers.net_labels(net, seed, rows)
+    assert digest(x) == str(g["x_digest"])
+    m = oracle.Model(net, helpers.net_weights(name, seed, std=0.1))
+    losses = np.array([m.train_step(x, y, lr) for lr in curve_lrs(base)], dtype=np.float32)
+    assert helpers.bitwise_equal(losses, g["losses"])
+    assert digest(m.w) == str(g["w_final_digest"])

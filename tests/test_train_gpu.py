@@ -1,0 +1,180 @@
+"""AOT training through ns_runtime_train_step on the GPU against the
+reference: per-step losses and trained weights (fixtures written by the
+reference build), every gradient of a step against the oracle, the Muon
+update on its determined part, the objective's purity, and 100-step loss
+curves with the cosine warmup schedule applied by the host.
+
+Loss tolerance.  Muon orthonormalises the gradient with modified
+Gram-Schmidt and its +1e-30 guard turns the rounding residue of every
+rank-deficient direction into a unit vector (LayerNorm outputs and
+softmax-minus-one-hot rows sum to zero, small batches have low rank), so the
+reference's own trajectory moves under a mere change of summation order.
+Each fixture records that movement (`band`: the largest deviation of the
+reference restatement with its MGS dot products summed in 2, 3, 4 or 8
+interleaved partial sums, tests/golden/make_band.py); a loss at step t must
+be within 1e-3 + 2 * max(band[:t+1]) of the reference.  AdamW-only
+networks have band 0, i.e. plain 1e-3, and their weights are compared too."""
+import os
+
+import numpy as np
+import pytest
+
+import helpers
+import oracle
+from golden.make_golden import CASES, CURVES, case_inputs, curve_lrs
+from neuralscript_amd import runtime
+
+pytestmark = pytest.mark.gpu
+
+TRAIN = [c for c in CASES if c[3]]
+LOSS_TOL = 1e-3
+
+
+def loss_tol(band):
+    return LOSS_TOL + 2.0 * np.maximum.accumulate(np.asarray(band, np.float64))
+
+
+def golden(name):
+    return np.load(os.path.join(helpers.GOLDEN, f"{name}.npz"))
+
+
+@pytest.mark.parametrize("case", TRAIN, ids=lambda c: c[0])
+def test_train_steps_match_reference_fixture(case):
+    name, rows, seed, steps, lr, _ = case
+    print(f"train {name} rows={rows} steps={steps}", flush=True)
+    net, x, y = case_inputs(name, rows, seed)
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, seed))
+    g = golden(name)
+    losses = np.array([lib.train_step(m, x, y, lr) for _ in range(steps)], dtype=np.float32)
+    tol = loss_tol(g["band"])
+    print(f"  losses {losses} reference {g['losses']} tolerance {tol}")
+    assert np.all(np.abs(losses - g["losses"]) <= tol), (losses, g["losses"], tol)
+    # the first loss is a pure forward: fp32 tolerance
+    helpers.assert_close(losses[:1], g["losses"][:1], f"{name} first loss")
+    obj = lib.objective_loss(m, x, y)
+    assert abs(obj - g["objective"]) <= tol[-1] + 2.0 * np.max(g["band"])
+    if not np.any(g["band"]):  # no Muon matrix: weights and outputs are determined
+        helpers.assert_close(lib.get_weights(m), g["w_final"], f"{name} trained weights", atol=1e-4, rtol=1e-3)
+        helpers.assert_close(lib.eval_infer(m, x)[: g["out_after"].size], g["out_after"], f"{name} forward after",
+                             atol=1e-4, rtol=1e-3)
+    lib.free(m)
+
+
+def test_objective_does_not_mutate_weights():
+    name, rows, seed = "c5t", 33, 108
+    net, x, y = case_inputs(name, rows, seed)
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, seed))
+    lib.train_step(m, x, y, 0.01)
+    w0 = lib.get_weights(m)
+    lib.objective_loss(m, x, y)
+    lib.objective_loss(m, x, y)
+    assert helpers.bitwise_equal(lib.get_weights(m), w0)
+    lib.free(m)
+
+
+def test_adamw_training_matches_oracle_step_by_step():
+    """AdamW network (xor): after every step the weights stay within fp32
+    tolerance of the oracle's (no drift accumulation)."""
+    name, rows, seed = "xor", 4, 103
+    net, x, y = case_inputs(name, rows, seed)
+    w = helpers.net_weights(name, seed)
+    om = oracle.Model(net, w)
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    for step in range(8):
+        lg = lib.train_step(m, x, y, 0.3)
+        lo = om.train_step(x, y, 0.3)
+        assert abs(lg - lo) <= 1e-5 + 1e-4 * abs(lo), (step, lg, lo)
+        helpers.assert_close(lib.get_weights(m), om.w, f"xor step {step}", atol=2e-5, rtol=2e-4)
+    lib.free(m)
+
+
+@pytest.mark.parametrize("curve", CURVES, ids=lambda c: f"{c[0]}-{c[2]}")
+def test_100_step_loss_curve_matches_reference(curve):
+    name, rows, seed, base = curve
+    print(f"curve {name} tokens={rows} lr={base}", flush=True)
+    g = np.load(os.path.join(helpers.GOLDEN, f"curve_{name}_{seed}.npz"))
+    net = oracle.Net(helpers.ir_text(name))
+    x = helpers.net_inputs(net, name, seed, rows)
+    y = helpers.net_labels(net, seed, rows)
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, seed, std=0.1))
+    losses = np.array([lib.train_step(m, x, y, lr) for lr in curve_lrs(base)], dtype=np.float32)
+    lib.free(m)
+    dev = np.abs(losses - g["losses"])
+    tol = loss_tol(g["band"])
+    print(f"  max |loss - reference| = {dev.max():.3g} at step {int(dev.argmax())}; "
+          f"reordering band max {g['band'].max():.3g}; worst ratio to tolerance {np.max(dev / tol):.3g}")
+    assert np.all(dev <= tol), (dev, tol)
+
+
+@pytest.mark.parametrize("name,rows", [("c5t", 40), ("mlpt", 17), ("c5s", 64), ("moet", 41), ("moet", 300)])
+def test_every_value_of_one_train_step_matches_oracle(name, rows):
+    """Each intermediate and gradient of one training step (read back from
+    the device by IR value name) against the oracle's value of the same
+    name; the weights after the optimizer last."""
+    ir = helpers.ir_text(name)
+    net = oracle.Net(ir)
+    seed = 400 + rows
+    x = helpers.net_inputs(net, name, seed, rows)
+    y = helpers.net_labels(net, seed, rows)
+    w = helpers.net_weights(name, seed)
+    om = oracle.Model(net, w)
+    rec = {}
+    om.train_step(x, y, 0.02, rec)
+    model = runtime.Model(runtime.Plan(ir), w)
+    model.train_step(x, y, 0.02)
+    bad = []
+    for ins in net.train.instrs:
+        v = ins.result
+        if v is None or v not in rec["buf"] or ins.op in ("ns.cross_entropy",):
+            continue
+        ref = rec["buf"][v]
+        got = model.read_value(v, ref.size)
+        viol = helpers.violation(got, ref, atol=1e-5, rtol=1e-3)
+        print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g}")
+        if viol > 1:
+            bad.append((ins.op, v, viol))
+    # Weights after the optimizer.  AdamW: the whole update.  Muon: the update
+    # is lr*sqrt(min(r,c))*Q + 0.01*lr*W with Q = MGS(grad); only the Q
+    # vectors of the determined prefix (rank of the gradient's vector set)
+    # are implementation-independent, the rest normalise rounding residue.
+    grads = {}
+    for ins in net.train.instrs:
+        if ins.op == "ns.opt.step":
+            grads = {ins.operands[k]: ins.operands[k + 1] for k in range(0, len(ins.operands) - 1, 2)}
+    lr = np.float32(0.02)
+    for n_, r, c in net.weights:
+        o = net.offsets[n_]
+        w0, wg, wo = w[o:o + r * c], model.read_value(n_, r * c), om.w[o:o + r * c]
+        if not oracle.use_muon(r, c):
+            v = helpers.violation(wg, wo, atol=2e-5, rtol=2e-4)
+            print(f"  weight {n_} [{r}x{c}] AdamW violation x{v:.3g}")
+            assert v <= 1, n_
+            continue
+        le = np.float64(lr) * np.sqrt(np.float32(min(r, c)))
+        decay = 0.01 * np.float64(lr)
+        qg = ((w0.astype(np.float64) - wg) - decay * w0) / le
+        qo = ((w0.astype(np.float64) - wo) - decay * w0) / le
+        G = rec["buf"][grads[n_]].reshape(r, c).astype(np.float64)
+        vecs = G if r < c else G.T           # one vector per row of `vecs`
+        qg = qg.reshape(r, c) if r < c else qg.reshape(r, c).T
+        qo = qo.reshape(r, c) if r < c else qo.reshape(r, c).T
+        # determined prefix: vectors whose Gram-Schmidt residual keeps > 1e-3
+        # of their norm, in order
+        basis, k = [], 0
+        for vj in vecs:
+            res = vj.copy()
+            for b in basis:
+                res -= (b @ res) * b
+            if np.linalg.norm(res) <= 1e-3 * max(np.linalg.norm(vj), 1e-30):
+                break
+            basis.append(res / np.linalg.norm(res))
+            k += 1
+        d = np.max(np.abs(qg[:k] - qo[:k])) if k else 0.0
+        print(f"  weight {n_} [{r}x{c}] Muon: determined vectors {k}/{vecs.shape[0]}, max |dQ| {d:.3g}")
+        assert d <= 2e-3, n_
+    assert not bad, bad
+    model.free()
