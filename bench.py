@@ -136,6 +136,50 @@ def bench_forward(key, steps, warmup):
             "kernels": kernels}
 
 
+def c5_work(M=16384, D=512, H=8, V=8192, FF=2048, C=8192):
+    """Algorithmic FLOP of one c5 training step (attention counted once)."""
+    dense_fwd = 2.0 * M * (4 * D * D + D * FF + FF * D + D * C)
+    return {"dense": 3 * dense_fwd, "attention": 4.0 * M * M * D * 3, "total": 3 * dense_fwd + 12.0 * M * M * D}
+
+
+def bench_train(key, steps, warmup):
+    """Device-resident training steps of config `key` (nsh_train_step_device);
+    lr = 3e-4 times the cosine-warmup multiplier, as the host applies it."""
+    from neuralscript_amd import runtime, workloads
+    if not runtime.has_gpu():
+        raise SystemExit("bench.py: no GPU visible to libnship")
+    wl = workloads.CONFIGS[key]
+    plan = runtime.Plan.load(wl.net)
+    w = workloads.weights(key, plan.layout(), workloads.ir_shapes(plan.ir))
+    dx = runtime.DeviceArray.from_host(workloads.inputs(key))
+    dy = runtime.DeviceArray.from_host(workloads.labels(key))
+    model = runtime.Model(plan, w)
+    scale = lambda t: min(1.0, t / 100.0)  # noqa: E731  (warmup ramp; t < 100 here)
+    t = 0
+    for _ in range(warmup):
+        model.train_step_device(dx, dy, 3e-4 * scale(t), want_loss=False)
+        t += 1
+    model.sync()
+    model.profile(True)
+    model.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.train_step_device(dx, dy, 3e-4 * scale(t), want_loss=False)
+        t += 1
+    model.sync()
+    dt = time.perf_counter() - t0
+    prof = model.profile_report()
+    loss = model.train_step_device(dx, dy, 3e-4 * scale(t))
+    model.free()
+    work = c5_work()
+    kernels = {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["calls"] / steps} for k, v in prof.items()}
+    return {"metric": METRIC, "value": steps / dt, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device"},
+            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss), "kernels": kernels}
+
+
 def bench_c2(steps, warmup, with_cpu):
     from neuralscript_amd import runtime, workloads
     if not runtime.has_gpu():
@@ -209,8 +253,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4"],
-                    help="c2 (default) is the metric's workload; c3/c4 print per-kernel breakdowns")
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"],
+                    help="c2 (default) is the metric's workload; c3/c4 (forward) and c5 (training steps) "
+                         "print per-kernel breakdowns")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -218,6 +263,8 @@ def main():
                          "see DESIGN.md for how the path would shard)")
     if a.config == "c2":
         res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
+    elif a.config == "c5":
+        res = bench_train(a.config, a.steps, a.warmup)
     else:
         res = bench_forward(a.config, a.steps, a.warmup)
     print(json.dumps(res), flush=True)
