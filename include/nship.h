@@ -119,6 +119,16 @@ int nsh_profile_report(ns_model* m, char* buf, size_t len);
 int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, int transA, int transB, int act);
 
+/* nsh_op_gemm with K split into `splits` chunks (0: the runtime's heuristic,
+ * the one its plans use): per-chunk partials into `workspace`, summed in
+ * chunk order, then the activation; the same operation as nsh_op_gemm, with
+ * the reduction over k reassociated.  The workspace holds
+ * nsh_op_gemm_splitk_workspace(...) bytes. */
+size_t nsh_op_gemm_splitk_workspace(int64_t M, int64_t N, int64_t K, int splits);
+int nsh_op_gemm_splitk(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                       int64_t lda, int64_t ldb, int64_t ldc, int transA, int transB, int act, int splits,
+                       void* workspace);
+
 /* out[i,:] = W[row(idx[i]),:], out-of-range or non-integral-range ids -> row 0;
  * ns_embedding, codegen.cpp:1711-1718. */
 int nsh_op_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D);
@@ -153,6 +163,19 @@ int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_
  * of ns_attention_fwd, codegen.cpp:1724-1777. */
 int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
                          int64_t D, int64_t H);
+
+/* Backward of the attention core: dQ, dK, dV [S, D] from Q, K, V, the
+ * forward's ctx (O), dO = d ctx and lse (nsh_op_attention_fwd's), i.e. per
+ * head the gradient of softmax(Q K^T / sqrt(D/H)) V; the core of the
+ * ATTENTION_GRAD_* kernels, codegen.cpp:1785-1907.  workspace: bytes from
+ * nsh_op_attention_bwd_workspace(S, D, H, store_ds).  store_ds != 0 keeps dS
+ * (H*S*S floats, when S % 64 == 0 and the head size is 32 or 64) so that dQ
+ * is one product over it instead of a pass that recomputes S and dP; the
+ * result is the same to fp32 rounding. */
+size_t nsh_op_attention_bwd_workspace(int64_t S, int64_t D, int64_t H, int store_ds);
+int nsh_op_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                         const float* lse, float* dQ, float* dK, float* dV, int64_t S, int64_t D, int64_t H,
+                         int store_ds, void* workspace);
 
 /* Modified Gram-Schmidt of g [r,c] over columns (r >= c) or rows (r < c),
  * q = the orthonormal result in g's layout; ns_orthonom, codegen.cpp:1617-1633.

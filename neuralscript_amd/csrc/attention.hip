@@ -314,13 +314,15 @@ struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
   }
 };
 
-template <int DK>
+// STORE_DS: also write dS = P o (dP - delta) (unscaled) to dS[h][query][key]
+// for flash_bwd_dq_ds_kernel; requires S % 64 == 0.
+template <int DK, bool STORE_DS>
 __global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                              const float* __restrict__ V, const float* __restrict__ dO,
                                                              const float* __restrict__ lse,
                                                              const float* __restrict__ delta, float* __restrict__ dK,
-                                                             float* __restrict__ dV, int S, int H, int64_t ld,
-                                                             float scale, float c_log2, int nkb) {
+                                                             float* __restrict__ dV, float* __restrict__ dS, int S,
+                                                             int H, int64_t ld, float scale, float c_log2, int nkb) {
   using Tile = QTile<DK>;
   constexpr int NDB = DK / 32;
   __shared__ __attribute__((aligned(16))) float sm[2 * Tile::kFloats];
@@ -386,6 +388,13 @@ __global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __rest
         const float p = key < S ? exp2f(sc[v] * c_log2 - ls[qr]) : 0.f;
         sc[v] = p;
         dp[v] = p * (dp[v] - ds[qr]);
+      }
+      if (STORE_DS && key < S) {
+        // lanes 0-31 / 32-63 write 32 consecutive keys of one query row each;
+        // every query row of the tile exists (S % 64 == 0)
+        float* __restrict__ dst = dS + ((int64_t)h * S + it * 64 + qb * 32 + 4 * kh) * S + key;
+#pragma unroll
+        for (int v = 0; v < 16; v++) dst[(int64_t)(8 * (v >> 2) + (v & 3)) * S] = dp[v];
       }
       // dV += P^T dO, dK += dS^T Q: step s pairs query 8(s/4) + 4kh + s%4.
 #pragma unroll
@@ -514,6 +523,125 @@ __global__ __launch_bounds__(256) void flash_bwd_dq_kernel(const float* __restri
   }
 }
 
+// One 64-key step of flash_bwd_dq_ds_kernel: the K tile (float4 i of thread
+// t is key (t + 256 i) / (DK/4), dims 4 ((t + 256 i) % (DK/4))) and this
+// lane's dS operands, d[4 kb + j] = keys key0 + 32 kb + 8 j + 4 kh + (0..3)
+// of its query row (drow already includes the 4 kh offset).
+template <int DK>
+struct DsTile {
+  static constexpr int P = DK + 4;
+  static constexpr int kPer = kBK * DK / 4 / 256;
+  float4 k[kPer], d[8];
+  __device__ void load(const float* __restrict__ K, const float* __restrict__ drow, int64_t ld, int hcol, int key0,
+                       bool qin, int t) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      k[i] = *reinterpret_cast<const float4*>(K + (int64_t)(key0 + idx / (DK / 4)) * ld + hcol + (idx % (DK / 4)) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      d[i] = keep4(qin, *reinterpret_cast<const float4*>(drow + key0 + 32 * (i >> 2) + 8 * (i & 3)));
+  }
+  __device__ void store_k(float* __restrict__ ks, int t) const {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<float4*>(ks + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = k[i];
+    }
+  }
+};
+
+// dQ = scale * dS K from the stored dS (S % 64 == 0): the dq kernel's
+// transposed product dQ^T += K^T dS^T without recomputing S and dP.  Lane =
+// query; its dS operands are 8 float4 per 64-key tile read straight from its
+// row (prefetched one tile ahead); K tiles go through LDS.
+template <int DK>
+__global__ __launch_bounds__(256) void flash_bwd_dq_ds_kernel(const float* __restrict__ K,
+                                                              const float* __restrict__ dS, float* __restrict__ dQ,
+                                                              int S, int H, int64_t ld, float scale, int nqb) {
+  constexpr int NDB = DK / 32;
+  constexpr int P = DK + 4;
+  __shared__ __attribute__((aligned(16))) float sm[2 * kBK * P > 4 * 32 * (DK + 1) ? 2 * kBK * P : 4 * 32 * (DK + 1)];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int L = remap_xcd(blockIdx.x, nqb * H);
+  const int h = L / nqb, q0 = (L % nqb) * kBQ;
+  const int hcol = h * DK;
+  const int qrow = q0 + w * 32 + l32;
+  const bool qin = qrow < S;
+  const float* __restrict__ drow = dS + ((int64_t)h * S + (qin ? qrow : S - 1)) * S + 4 * kh;
+  floatx16 acc[NDB];
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[d][v] = 0.f;
+
+  DsTile<DK> tile;
+  const int nkv = S / kBK;
+  tile.load(K, drow, ld, hcol, 0, qin, t);
+  tile.store_k(sm, t);
+  __syncthreads();
+  for (int it = 0; it < nkv; it++) {
+    const int cur = it & 1;
+    const bool more = it + 1 < nkv;
+    float dv[32];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      dv[4 * i] = tile.d[i].x; dv[4 * i + 1] = tile.d[i].y; dv[4 * i + 2] = tile.d[i].z; dv[4 * i + 3] = tile.d[i].w;
+    }
+    // unconditional (the last step reloads its own tile) so that the tile
+    // stays in registers
+    tile.load(K, drow, ld, hcol, (more ? it + 1 : it) * kBK, qin, t);
+  const float* ks = sm + cur * kBK * P;
+    // step s of key block kb pairs key 32kb + 8(s/4) + 4kh + s%4 = dv[16kb + s]
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int s2 = 0; s2 < 16; s2++) {
+        const int kr = kb * 32 + 8 * (s2 >> 2) + 4 * kh + (s2 & 3);
+#pragma unroll
+        for (int d = 0; d < NDB; d++)
+          acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[kr * P + d * 32 + l32], dv[16 * kb + s2], acc[d], 0, 0, 0);
+      }
+    tile.store_k(sm + (cur ^ 1) * kBK * P, t);
+    __syncthreads();
+  }
+  // dQ^T (d, query) -> LDS [query][d] -> rows of dQ
+  float* T = sm + w * 32 * (DK + 1);
+#pragma unroll
+  for (int d = 0; d < NDB; d++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) T[l32 * (DK + 1) + d * 32 + 8 * (v >> 2) + 4 * kh + (v & 3)] = acc[d][v] * scale;
+  __syncthreads();
+  for (int r = 0; r < 32; r++) {
+    const int q = q0 + w * 32 + r;
+    if (q >= S) break;
+    for (int c = lane; c < DK; c += 64) dQ[(int64_t)q * ld + hcol + c] = T[r * (DK + 1) + c];
+  }
+}
+
+// delta for DK in {32, 64} on 16-byte aligned rows: one wave per query row,
+// one float4 per lane and pass, DK/4 lanes per head (a head's lanes are all
+// in or all out of a pass, so the shuffles stay among active lanes).
+template <int DK>
+__global__ __launch_bounds__(256) void attn_delta_rows_kernel(const float* __restrict__ dO,
+                                                              const float* __restrict__ O, float* __restrict__ delta,
+                                                              int S, int H, int64_t ld) {
+  constexpr int LPH = DK / 4;
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (q >= S) return;
+  const int D = H * DK;
+  for (int c = lane * 4; c < D; c += 256) {
+    const float4 a = *reinterpret_cast<const float4*>(dO + (int64_t)q * ld + c);
+    const float4 b = *reinterpret_cast<const float4*>(O + (int64_t)q * ld + c);
+    float p = a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+#pragma unroll
+    for (int o = LPH / 2; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
+    if ((lane & (LPH - 1)) == 0) delta[(int64_t)(c / DK) * S + q] = p;
+  }
+}
+
 // Any head size up to 128 (test networks): one thread per (row, head).
 // Pass 1 (per query): dQ.  Pass 2 (per key): dK, dV.
 __global__ __launch_bounds__(64) void attn_bwd_small_q_kernel(const float* __restrict__ Q, const float* __restrict__ K,
@@ -606,9 +734,18 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
   return 0;
 }
 
+size_t attention_bwd_ds_floats(int64_t S, int64_t D, int64_t H) {
+  if (S <= 0 || H <= 0 || D % H != 0 || S % kBK != 0) return 0;
+  const int64_t DK = D / H;
+  if (DK != 32 && DK != 64) return 0;
+  const double bytes = 4.0 * (double)H * (double)S * (double)S;
+  if (bytes > 16.0 * 1024 * 1024 * 1024) return 0;  // recompute beyond 16 GiB
+  return (size_t)(H * S * S);
+}
+
 int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                          const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, hipStream_t s) {
+                         int64_t H, int64_t ld, float* ds_ws, hipStream_t s) {
   if (S <= 0) return 0;
   if (H <= 0 || D % H != 0 || S > INT32_MAX) {
     set_error("attention backward: bad shape");
@@ -621,24 +758,41 @@ int launch_attention_bwd(const float* Q, const float* K, const float* V, const f
   }
   const float scale = 1.0f / sqrtf((float)DK);
   const float cl2 = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)ceil_div(S * H, 256)), dim3(256), 0, s, dO, O, delta, (int)S,
-                     (int)H, (int)DK, ld);
+  const bool aligned =
+      ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)dO | (uintptr_t)O) % 16 == 0;
+  const bool flash = aligned && (DK == 64 || DK == 32);
+  if (flash) {
+    const dim3 g((unsigned)ceil_div(S, 4));
+    if (DK == 64)
+      hipLaunchKernelGGL(attn_delta_rows_kernel<64>, g, dim3(256), 0, s, dO, O, delta, (int)S, (int)H, ld);
+    else
+      hipLaunchKernelGGL(attn_delta_rows_kernel<32>, g, dim3(256), 0, s, dO, O, delta, (int)S, (int)H, ld);
+  } else {
+    hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)ceil_div(S * H, 256)), dim3(256), 0, s, dO, O, delta, (int)S,
+                       (int)H, (int)DK, ld);
+  }
   NSH_LAUNCHED();
-  const bool aligned = ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)dO) % 16 == 0;
-  if (aligned && (DK == 64 || DK == 32)) {
+  if (flash) {
     const int nb = (int)ceil_div(S, kBQ);
     const dim3 grid(nb * (unsigned)H), block(256);
+    const bool use_ds = ds_ws && attention_bwd_ds_floats(S, D, H) > 0 && ((uintptr_t)ds_ws % 16) == 0;
+#define NSH_BWD(DK_)                                                                                                  \
+  if (use_ds) {                                                                                                       \
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK_, true>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, ds_ws, \
+                       (int)S, (int)H, ld, scale, cl2, nb);                                                           \
+    hipLaunchKernelGGL(flash_bwd_dq_ds_kernel<DK_>, grid, block, 0, s, K, ds_ws, dQ, (int)S, (int)H, ld, scale, nb); \
+  } else {                                                                                                            \
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK_, false>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV,      \
+                       nullptr, (int)S, (int)H, ld, scale, cl2, nb);                                                  \
+    hipLaunchKernelGGL(flash_bwd_dq_kernel<DK_>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,  \
+                       scale, cl2, nb);                                                                               \
+  }
     if (DK == 64) {
-      hipLaunchKernelGGL(flash_bwd_dkdv_kernel<64>, grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
-                         ld, scale, cl2, nb);
-      hipLaunchKernelGGL(flash_bwd_dq_kernel<64>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,
-                         scale, cl2, nb);
+      NSH_BWD(64)
     } else {
-      hipLaunchKernelGGL(flash_bwd_dkdv_kernel<32>, grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
-                         ld, scale, cl2, nb);
-      hipLaunchKernelGGL(flash_bwd_dq_kernel<32>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,
-                         scale, cl2, nb);
+      NSH_BWD(32)
     }
+#undef NSH_BWD
   } else {
     const dim3 grid((unsigned)ceil_div(S * H, 64));
     hipLaunchKernelGGL(attn_bwd_small_q_kernel, grid, dim3(64), 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H,

@@ -158,6 +158,11 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
     kbeg = g.kseg[blockIdx.y];
     kend = g.kseg[blockIdx.y + 1];
   }
+  if (g.kchunk) {
+    kbeg = (int)blockIdx.z * g.kchunk;
+    kend = min(K, kbeg + g.kchunk);
+    C += (int64_t)blockIdx.z * g.sCk;
+  }
   constexpr bool AKC = !TA, BKC = TB;
   constexpr int ASZ = TileLayout<AKC>::kSize, BSZ = TileLayout<BKC>::kSize;
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
@@ -276,13 +281,76 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   g.tiles_n = (int)ceil_div(g.N, BN);
   // grouped: an upper bound on tile entries, sum_e ceil(n_e / BM) <= M/BM + E
   const int entries = g.groups ? g.tiles_m + g.groups : g.tiles_m;
-  const dim3 grid(entries * g.tiles_n, batch), block(NT);
+  const int zs = g.kchunk ? (int)ceil_div(g.K, g.kchunk) : 1;
+  const dim3 grid(entries * g.tiles_n, batch, zs), block(NT);
 #define NSH_GEMM(TA_, TB_, V_) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_>), grid, block, 0, s, g)
   if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
   else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
   else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
   else { if (vec) NSH_GEMM(true, true, true); else NSH_GEMM(true, true, false); }
 #undef NSH_GEMM
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// Sum of the K-chunk partials in chunk order, then the GEMM's epilogue.
+// ws holds [splits][batch][M][N]; thread per output element.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int splits, int64_t zstride,
+                                                            GemmArgs g) {
+  const int64_t n_out = (int64_t)g.M * g.N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_out) return;
+  const int y = blockIdx.y;
+  const int64_t off = (int64_t)y * n_out + i;
+  float a = 0.f;
+  for (int z = 0; z < splits; z++) a += ws[(int64_t)z * zstride + off];
+  const int row = (int)(i / g.N), col = (int)(i % g.N);
+  float* dst = g.C + (int64_t)y * g.sC + (int64_t)row * g.ldc + col;
+  if (g.mode == kEpiAct) *dst = act_apply(a, g.act);
+  else if (g.mode == kEpiActGrad) *dst = a * act_deriv(g.aux[(int64_t)row * g.ldaux + col], g.act);
+  else *dst = *dst + a;
+}
+
+static bool splittable(const GemmArgs& g) {
+  return !g.groups && !g.kseg && !g.a_rows && !g.c_rows && !g.row_scale && g.kchunk == 0;
+}
+
+// Chunk length for `splits` chunks: a multiple of BK (and so of 4, keeping
+// float4 staging aligned).
+static int split_chunk(int K, int splits) { return (int)(ceil_div(ceil_div(K, splits), BK) * BK); }
+
+int gemm_split_count(const GemmArgs& g, int batch) {
+  if (!splittable(g) || g.M <= 0 || g.N <= 0 || batch <= 0) return 1;
+  const int64_t tiles = ceil_div(g.M, BM) * ceil_div(g.N, BN) * batch;
+  if (tiles >= 384) return 1;
+  int64_t sp = std::min<int64_t>(ceil_div(768, tiles), g.K / 512);
+  sp = std::min<int64_t>(sp, 32);
+  if (sp < 2) return 1;
+  return (int)ceil_div(g.K, split_chunk(g.K, (int)sp));
+}
+
+size_t gemm_split_workspace(const GemmArgs& g, int batch, int splits) {
+  return splits <= 1 ? 0 : (size_t)splits * batch * g.M * g.N;
+}
+
+int launch_gemm_split(const GemmArgs& in, bool tA, bool tB, int batch, int splits, float* ws, hipStream_t s) {
+  if (splits <= 1 || !ws || !splittable(in) || in.K < 2 * BK) return launch_gemm_ex(in, tA, tB, batch, s);
+  if (in.M <= 0 || in.N <= 0 || batch <= 0) return 0;
+  const int chunk = split_chunk(in.K, splits);
+  const int zs = (int)ceil_div(in.K, chunk);
+  const int64_t n_out = (int64_t)in.M * in.N;
+  GemmArgs p = in;
+  p.C = ws;
+  p.ldc = in.N;
+  p.sC = n_out;
+  p.mode = kEpiAct;
+  p.act = 0;
+  p.aux = nullptr;
+  p.kchunk = chunk;
+  p.sCk = n_out * batch;
+  if (launch_gemm_ex(p, tA, tB, batch, s) != 0) return -1;
+  const dim3 grid((unsigned)ceil_div(n_out, 256), batch);
+  hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, s, ws, zs, n_out * batch, in);
   NSH_LAUNCHED();
   return 0;
 }

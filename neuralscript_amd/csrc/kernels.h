@@ -40,10 +40,22 @@ struct GemmArgs {
   // K-grouped mode (kseg set): launch with batch = groups; group y contracts
   // over k in [kseg[y], kseg[y+1]) and writes C + y * sC.
   const int* kseg = nullptr;
+  // Split K (kchunk > 0): blockIdx.z contracts over k in
+  // [z * kchunk, min(K, (z+1) * kchunk)) and writes C + z * sCk.
+  int kchunk = 0;
+  int64_t sCk = 0;
   int tiles_m = 0, tiles_n = 0;    // filled by the launcher
 };
 
 int launch_gemm_ex(const GemmArgs& g, bool tA, bool tB, int batch, hipStream_t s);
+// Split-K for GEMMs with few output tiles and a long K: number of K chunks
+// the heuristic picks (1 = no split) and the workspace it needs (floats).
+int gemm_split_count(const GemmArgs& g, int batch);
+size_t gemm_split_workspace(const GemmArgs& g, int batch, int splits);
+// Runs g with `splits` K chunks through `ws` (partials, then a fixed-order
+// reduction applying g's epilogue); splits <= 1 or a plan the split does not
+// support (row gather/scatter, groups) runs launch_gemm_ex.
+int launch_gemm_split(const GemmArgs& g, bool tA, bool tB, int batch, int splits, float* ws, hipStream_t s);
 int launch_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
                 int64_t lda, int64_t ldb, int64_t ldc, bool tA, bool tB, int act, hipStream_t s);
 
@@ -67,10 +79,14 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
                          int64_t H, int64_t ld, hipStream_t s);
 
 // Backward of the core: dQ, dK, dV [S, D] (row pitch ld) from dO = d ctx, the
-// forward's ctx (O) and lse; delta: [H, S] workspace.
+// forward's ctx (O) and lse; delta: [H, S] workspace.  ds_ws (optional, 16-byte
+// aligned, attention_bwd_ds_floats(S, D, H) floats when that is nonzero)
+// holds dS so that dQ is a product over it instead of a second pass that
+// recomputes S and dP.
+size_t attention_bwd_ds_floats(int64_t S, int64_t D, int64_t H);
 int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                          const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, hipStream_t s);
+                         int64_t H, int64_t ld, float* ds_ws, hipStream_t s);
 
 // optim.hip --------------------------------------------------------------------
 int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1t, float b2t,
@@ -80,16 +96,17 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
 struct MuonMat {
   float* w;          // weight [r][c], updated in place
   const float* g;    // gradient [r][c]
-  float* T;          // work: vectors contiguous, [C][R]
-  float* norms;      // [C]
+  float* T;          // work: vectors contiguous, [C][R]; q vectors on exit
+  float* norms;      // [C] (per-column path)
   int R, C;          // vector length, number of vectors
   int transposed;    // r < c: the vectors are the rows of g
-  int nblk;          // workgroups of this matrix in each MGS step launch
+  int nblk;          // workgroups of this matrix in each per-column MGS launch
   float le, decay;   // lr * sqrt(min(r, c)), 0.01 * lr
 };
 int muon_blocks(int C);
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
-int launch_mgs_steps(const MuonMat* d_mats, int nmat, int total_blocks, int max_c, hipStream_t s);
+// MGS of every matrix: T holds the vectors on entry, the q vectors on exit.
+int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s);
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 
 // moe.hip ----------------------------------------------------------------------

@@ -13,22 +13,29 @@
 // apply, so m = g; Q = MGS(g) over columns (r >= c) or rows (r < c),
 // ns_orthonom codegen.cpp:1617-1633; w -= lr sqrt(min(r,c)) Q + (0.01 lr) w.
 //
-// MGS on the GPU, right-looking: at step j every later vector v_c is
-// projected against q_j = v_j / (|v_j| + 1e-30).  Each vector receives the
-// same projections in the same order as in the reference's left-looking
-// loop; only the order inside each dot product differs (tree reductions).
-// All Muon matrices of the step advance together: one launch per column
-// index j, each workgroup owning a few later vectors of one matrix and
-// recomputing |v_j| itself (same reduction tree in every workgroup, so every
-// workgroup sees the same norm).  Vectors are stored contiguously in a
-// work buffer T[C][R] (a transpose of g for r >= c).
+// MGS on the GPU, right-looking and blocked in panels of kPB vectors.  Every
+// vector receives the same projections in the same order as in the
+// reference's loop (q_0, q_1, ... q_{c-1}, then its own normalisation
+// v / (|v| + 1e-30)); only the order inside each dot product differs (per
+// thread partial sums, then a fixed tree).  One launch per panel: launch p
+// applies the projections of panel p to every later vector, kPB vectors per
+// workgroup held in registers, and the workgroup that owns panel p+1 then
+// factorizes it in registers and stores its normalised q vectors.  All Muon
+// matrices of the step advance together in the same launches.  Vectors live
+// contiguously in a work buffer T[C][R] (a transpose of g when r >= c).
+// Vectors longer than kMaxPanelR take the per-column path (one launch per
+// column, every workgroup recomputing |v_j| with the same tree).
 #include "common.h"
 #include "kernels.h"
 
 namespace nship {
 namespace {
 
-constexpr int kCPB = 4;  // later vectors per workgroup per step
+constexpr int kCPB = 4;  // later vectors per workgroup per step (per-column path)
+constexpr int kPB = 8;   // panel width (vectors per workgroup, panel path)
+constexpr int kPanelThreads = 1024;
+constexpr int kPanelWaves = kPanelThreads / 64;
+constexpr int kMaxPanelR = 8 * kPanelThreads;
 
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ w, const float* __restrict__ g,
                                                     float* __restrict__ m, float* __restrict__ v, int64_t n, float lr,
@@ -99,7 +106,171 @@ __global__ __launch_bounds__(256) void mgs_step_kernel(const MuonMat* __restrict
   }
 }
 
-// w -= le * q + (0.01 lr) * w with q = T / norm (the final normalisation).
+__global__ __launch_bounds__(256) void mgs_normalize_kernel(const MuonMat* __restrict__ mats, int nmat) {
+  const MuonMat& M = mats[blockIdx.y];
+  const int64_t n = (int64_t)M.R * M.C;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    M.T[i] = M.T[i] / M.norms[i / M.R];
+  (void)nmat;
+}
+
+// Sums NV values over the 1024 threads of a workgroup; every thread gets the
+// totals, identical in every lane.  Wave partials go to LDS; each wave then
+// re-reduces them with G = 64/NV lanes per value (fixed order) and broadcasts.
+// `red` alternates between two buffers in consecutive calls, so one barrier
+// per call suffices: a thread reads buffer b only before it reaches the
+// barrier of the next call, and buffer b is written again only after it.
+template <int NV>
+__device__ __forceinline__ void panel_sum(float (&v)[NV], float* red) {
+  static_assert(64 % NV == 0 && 64 / NV <= 64, "NV must divide 64");
+  constexpr int G = 64 / NV;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NV; i++) v[i] = wave_sum(v[i]);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) red[w * NV + i] = v[i];
+  }
+  __syncthreads();
+  const int i = lane / G, u0 = lane % G;
+  float p = 0.f;
+#pragma unroll
+  for (int u = 0; u < kPanelWaves; u += G)
+    if (u + u0 < kPanelWaves) p += red[(u + u0) * NV + i];
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
+#pragma unroll
+  for (int k = 0; k < NV; k++) v[k] = __shfl(p, k * G, 64);
+}
+
+// Elements of a vector held by thread t: VEC (R % 4 == 0, rows 16-byte
+// aligned): float4 chunks t + kPanelThreads * i, i < EPT / 4; otherwise
+// elements t + kPanelThreads * e.  Either way a wave's access is contiguous.
+template <int EPT, bool VEC>
+__device__ __forceinline__ void row_load(const float* __restrict__ row, int R, int t, bool valid,
+                                         float (&x)[EPT]) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < EPT / 4; i++) {
+      const int c = 4 * (t + kPanelThreads * i);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (valid && c < R) v = *reinterpret_cast<const float4*>(row + c);
+      x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      const int k = t + kPanelThreads * e;
+      x[e] = (valid && k < R) ? row[k] : 0.f;
+    }
+  }
+}
+
+template <int EPT, bool VEC>
+__device__ __forceinline__ void row_store(float* __restrict__ row, int R, int t, const float (&x)[EPT]) {
+  if constexpr (VEC) {
+#pragma unroll
+    for (int i = 0; i < EPT / 4; i++) {
+      const int c = 4 * (t + kPanelThreads * i);
+      if (c < R) *reinterpret_cast<float4*>(row + c) = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; e++) {
+      const int k = t + kPanelThreads * e;
+      if (k < R) row[k] = x[e];
+    }
+  }
+}
+
+// Launch for panel jp (jp < 0: the first launch, no projections): vectors
+// c >= jp + kPB, kPB per workgroup; workgroup 0 of each matrix owns the next
+// panel and factorizes it.
+template <int EPT, bool VEC>
+__global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat* __restrict__ mats, int nmat,
+                                                                   int jp) {
+  __shared__ float red[2][kPanelWaves * kPB];
+  const int first = jp + kPB;
+  int b = blockIdx.x, mi = 0;
+  for (; mi < nmat; mi++) {
+    const int nvec = mats[mi].C - first;
+    const int cnt = nvec <= 0 ? 0 : (jp < 0 ? 1 : (nvec + kPB - 1) / kPB);
+    if (b < cnt) break;
+    b -= cnt;
+  }
+  if (mi >= nmat) return;
+  const MuonMat& M = mats[mi];
+  const int R = M.R;
+  const int c0 = first + b * kPB;
+  const int nv = min(kPB, M.C - c0);
+  const int t = threadIdx.x;
+  float* __restrict__ T = M.T;
+  float x[kPB][EPT];
+#pragma unroll
+  for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, v < nv, x[v]);
+  int par = 0;
+  if (jp >= 0) {
+    // q_{jj+1} is fetched while q_jj's projections reduce.
+    float qn[EPT];
+    row_load<EPT, VEC>(T + (int64_t)jp * R, R, t, true, qn);
+#pragma unroll 1
+    for (int jj = 0; jj < kPB; jj++) {
+      float qv[EPT];
+#pragma unroll
+      for (int e = 0; e < EPT; e++) qv[e] = qn[e];
+      row_load<EPT, VEC>(T + (int64_t)(jp + jj + 1) * R, R, t, jj + 1 < kPB, qn);
+      float d[kPB];
+#pragma unroll
+      for (int v = 0; v < kPB; v++) {
+        d[v] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPT; e++) d[v] += qv[e] * x[v][e];
+      }
+      panel_sum<kPB>(d, red[par]);
+      par ^= 1;
+#pragma unroll
+      for (int v = 0; v < kPB; v++)
+#pragma unroll
+        for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * qv[e];
+    }
+  }
+  if (b == 0) {
+#pragma unroll
+    for (int jj = 0; jj < kPB; jj++) {
+      if (jj >= nv) break;
+      float s[1] = {0.f};
+#pragma unroll
+      for (int e = 0; e < EPT; e++) s[0] += x[jj][e] * x[jj][e];
+      panel_sum<1>(s, red[par]);
+      par ^= 1;
+      const float nrm = sqrtf(s[0]) + 1e-30f;
+#pragma unroll
+      for (int e = 0; e < EPT; e++) x[jj][e] /= nrm;
+      float d[kPB];
+#pragma unroll
+      for (int v = 0; v < kPB; v++) {
+        d[v] = 0.f;
+        if (v > jj) {
+#pragma unroll
+          for (int e = 0; e < EPT; e++) d[v] += x[jj][e] * x[v][e];
+        }
+      }
+      panel_sum<kPB>(d, red[par]);
+      par ^= 1;
+#pragma unroll
+      for (int v = 0; v < kPB; v++)
+        if (v > jj) {
+#pragma unroll
+          for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * x[jj][e];
+        }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < kPB; v++)
+    if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, x[v]);
+}
+
+// w -= le * q + (0.01 lr) * w, q = T (normalised vectors).
 __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restrict__ mats, int nmat) {
 #pragma clang fp contract(off)
   const MuonMat& M = mats[blockIdx.y];
@@ -109,7 +280,7 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restr
     int64_t j, k;
     if (M.transposed) { j = i / M.R; k = i % M.R; }
     else { k = i / M.C; j = i % M.C; }
-    const float q = M.T[j * M.R + k] / M.norms[j];
+    const float q = M.T[j * M.R + k];
     const float wi = M.w[i];
     M.w[i] = wi - (M.le * q + M.decay * wi);
   }
@@ -136,9 +307,45 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
   return 0;
 }
 
-int launch_mgs_steps(const MuonMat* d_mats, int nmat, int total_blocks, int max_c, hipStream_t s) {
-  for (int j = 0; j < max_c; j++) {
-    hipLaunchKernelGGL(mgs_step_kernel, dim3(total_blocks), dim3(256), 0, s, d_mats, nmat, j);
+int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s) {
+  if (nmat <= 0) return 0;
+  int max_r = 0, max_c = 0, col_blocks = 0;
+  int64_t max_elems = 0;
+  for (int i = 0; i < nmat; i++) {
+    max_r = std::max(max_r, h_mats[i].R);
+    max_c = std::max(max_c, h_mats[i].C);
+    col_blocks += h_mats[i].nblk;
+    max_elems = std::max(max_elems, (int64_t)h_mats[i].R * h_mats[i].C);
+  }
+  if (max_r > kMaxPanelR) {
+    for (int j = 0; j < max_c; j++) {
+      hipLaunchKernelGGL(mgs_step_kernel, dim3(col_blocks), dim3(256), 0, s, d_mats, nmat, j);
+      NSH_LAUNCHED();
+    }
+    const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 256), 2048);
+    hipLaunchKernelGGL(mgs_normalize_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
+    NSH_LAUNCHED();
+    return 0;
+  }
+  const int ept = max_r <= kPanelThreads ? 1 : max_r <= 2 * kPanelThreads ? 2 : max_r <= 4 * kPanelThreads ? 4 : 8;
+  bool vec = ept >= 4;
+  for (int i = 0; i < nmat; i++)
+    vec = vec && h_mats[i].R % 4 == 0 && (reinterpret_cast<uintptr_t>(h_mats[i].T) & 15) == 0;
+  for (int jp = -kPB; jp + kPB < max_c; jp += kPB) {
+    int grid = 0;
+    for (int i = 0; i < nmat; i++) {
+      const int nvec = h_mats[i].C - (jp + kPB);
+      if (nvec > 0) grid += jp < 0 ? 1 : (int)ceil_div(nvec, kPB);
+    }
+#define NSH_PANEL(E_, V_) \
+  hipLaunchKernelGGL((mgs_panel_kernel<E_, V_>), dim3(grid), dim3(kPanelThreads), 0, s, d_mats, nmat, jp)
+    switch (ept) {
+      case 1: NSH_PANEL(1, false); break;
+      case 2: NSH_PANEL(2, false); break;
+      case 4: if (vec) NSH_PANEL(4, true); else NSH_PANEL(4, false); break;
+      default: if (vec) NSH_PANEL(8, true); else NSH_PANEL(8, false); break;
+    }
+#undef NSH_PANEL
     NSH_LAUNCHED();
   }
   return 0;

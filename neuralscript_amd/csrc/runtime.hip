@@ -167,6 +167,30 @@ float* scratch(ns_model* m, const std::string& key, size_t n) {
   return b.p;
 }
 
+// GEMMs of the model's plan: split K through a grow-only workspace when the
+// output has too few tiles to fill the device (weight gradients).
+int rt_gemm_ex(ns_model* m, const GemmArgs& g, bool tA, bool tB, int batch) {
+  const int sp = gemm_split_count(g, batch);
+  if (sp <= 1) return launch_gemm_ex(g, tA, tB, batch, m->stream);
+  float* ws = scratch(m, "splitk", gemm_split_workspace(g, batch, sp));
+  if (!ws) return -1;
+  return launch_gemm_split(g, tA, tB, batch, sp, ws, m->stream);
+}
+
+int rt_gemm(ns_model* m, const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+            int64_t ldb, int64_t ldc, bool tA, bool tB, int act) {
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) {
+    set_error("gemm: dimension exceeds int32");
+    return -1;
+  }
+  GemmArgs g;
+  g.A = A; g.B = B; g.C = C;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+  g.act = act;
+  return rt_gemm_ex(m, g, tA, tB, 1);
+}
+
 // MoE work arrays for M tokens (grow-only scratch).
 int moe_work(ns_model* m, int64_t M, MoeWork* w) {
   const MoeInfo& q = m->plan->moe;
@@ -229,7 +253,7 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)K);
       NSH_OUT(C, I.res, (size_t)(M * N));
       Prof p(m, I.act ? "gemm_act" : "gemm");
-      return launch_gemm(fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, M, N, K, K, N, N, false, false, I.act, s);
+      return rt_gemm(m, fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, M, N, K, K, N, N, false, false, I.act);
     }
     case Op::Act: {
       const size_t n = fr.numel[I.in[0]];
@@ -288,12 +312,12 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
           g.B = fr.ptr[I.in[1]];
           g.C = sv.qkv;
           g.sA = 0; g.sB = D * D; g.sC = BS * D;
-          if (launch_gemm_ex(g, false, false, 3, s) != 0) return -1;
+          if (rt_gemm_ex(m, g, false, false, 3) != 0) return -1;
         } else {
           for (int j = 0; j < 3; j++) {
             g.B = fr.ptr[I.in[1 + j]];
             g.C = sv.qkv + j * BS * D;
-            if (launch_gemm_ex(g, false, false, 1, s) != 0) return -1;
+            if (rt_gemm_ex(m, g, false, false, 1) != 0) return -1;
           }
         }
       }
@@ -304,7 +328,7 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
           return -1;
       }
       Prof p(m, "gemm");
-      return launch_gemm(sv.ctx, fr.ptr[I.in[4]], out, BS, D, D, D, D, D, false, false, 0, s);
+      return rt_gemm(m, sv.ctx, fr.ptr[I.in[4]], out, BS, D, D, D, D, D, false, false, 0);
     }
     case Op::Moe: {
       const MoeInfo& q = P.moe;
@@ -409,14 +433,17 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
   {
     Prof p(m, "gemm");
     // dPre = dout Wo^T
-    if (launch_gemm(dout, Wo, dPre, BS, D, D, D, D, D, false, true, 0, s) != 0) return -1;
+    if (rt_gemm(m, dout, Wo, dPre, BS, D, D, D, D, D, false, true, 0) != 0) return -1;
     // dWo = ctx^T dout
-    if (launch_gemm(sv.ctx, dout, out->dWo, D, D, BS, D, D, D, true, false, 0, s) != 0) return -1;
+    if (rt_gemm(m, sv.ctx, dout, out->dWo, D, D, BS, D, D, D, true, false, 0) != 0) return -1;
   }
   {
     Prof p(m, "attention_bwd");
+    const size_t nds = attention_bwd_ds_floats(BS, D, H);
+    float* ds = nds ? scratch(m, "attn_ds", nds) : nullptr;
+    if (nds && !ds) return -1;
     if (launch_attention_bwd(sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, dPre, sv.lse, delta, dqkv,
-                             dqkv + BS * D, dqkv + 2 * BS * D, BS, D, H, D, s) != 0)
+                             dqkv + BS * D, dqkv + 2 * BS * D, BS, D, H, D, ds, s) != 0)
       return -1;
   }
   Prof p(m, "gemm");
@@ -426,7 +453,7 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
   g.M = (int)D; g.N = (int)D; g.K = (int)BS;
   g.lda = D; g.ldb = D; g.ldc = D;
   g.sA = 0; g.sB = BS * D; g.sC = D * D;
-  if (launch_gemm_ex(g, true, false, 3, s) != 0) return -1;
+  if (rt_gemm_ex(m, g, true, false, 3) != 0) return -1;
   // dX = dQ Wq^T + dK Wk^T + dV Wv^T
   const float* Ws[3] = {Wq, Wk, Wv};
   for (int j = 0; j < 3; j++) {
@@ -435,19 +462,18 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
     h.M = (int)BS; h.N = (int)D; h.K = (int)D;
     h.lda = D; h.ldb = D; h.ldc = D;
     h.mode = j == 0 ? kEpiAct : kEpiAccum;
-    if (launch_gemm_ex(h, false, true, 1, s) != 0) return -1;
+    if (rt_gemm_ex(m, h, false, true, 1) != 0) return -1;
   }
   return 0;
 }
 
 // Muon step of several matrices: descriptors to the device, gather, MGS
 // column steps, update.
-int muon_batch(MuonMat* d, const std::vector<MuonMat>& mats, int64_t max_elems, int max_c, int total_blocks,
-               hipStream_t s) {
+int muon_batch(MuonMat* d, const std::vector<MuonMat>& mats, int64_t max_elems, hipStream_t s) {
   const int nm = (int)mats.size();
   NSH_CHECK(hipMemcpyAsync(d, mats.data(), nm * sizeof(MuonMat), hipMemcpyHostToDevice, s));
   if (launch_muon_gather(d, nm, max_elems, s) != 0) return -1;
-  if (launch_mgs_steps(d, nm, total_blocks, max_c, s) != 0) return -1;
+  if (launch_mgs(d, mats.data(), nm, s) != 0) return -1;
   return launch_muon_update(d, nm, max_elems, s);
 }
 
@@ -456,7 +482,6 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
   hipStream_t s = m->stream;
   m->muon_host.clear();
   int64_t max_elems = 0;
-  int max_c = 0, total_blocks = 0;
   for (size_t k = 0; k + 1 < I.in.size(); k += 2) {
     const int wid = I.in[k], gid = I.in[k + 1];
     const Value& W = P.vals[wid];
@@ -483,8 +508,6 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
       mm.decay = 0.01f * lr;
       m->muon_host.push_back(mm);
       max_elems = std::max(max_elems, n);
-      max_c = std::max(max_c, mm.C);
-      total_blocks += mm.nblk;
     } else {
       auto& st = m->adam[wid];
       if (!st.m) {
@@ -504,7 +527,7 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
   MuonMat* d = reinterpret_cast<MuonMat*>(scratch(m, "muon_desc", (nm * sizeof(MuonMat) + 3) / 4));
   if (!d) return -1;
   Prof p(m, "muon");
-  return muon_batch(d, m->muon_host, max_elems, max_c, total_blocks, s);
+  return muon_batch(d, m->muon_host, max_elems, s);
 }
 
 int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, float lr, bool train_mode,
@@ -594,7 +617,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             NSH_OUT(C, res, (size_t)(M * K));
             g.C = C;
             Prof p(m, "gemm");
-            if (launch_gemm_ex(g, false, true, 1, s) != 0) return -1;
+            if (rt_gemm_ex(m, g, false, true, 1) != 0) return -1;
             break;
           }
           case Op::MatmulGradW: {
@@ -603,7 +626,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             const int64_t M = (int64_t)(fr.numel[I.in[1]] / (size_t)N);
             NSH_OUT(C, I.res, (size_t)(K * N));
             Prof p(m, "gemm");
-            if (launch_gemm(fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, K, N, M, K, N, N, true, false, 0, s) != 0) return -1;
+            if (rt_gemm(m, fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, K, N, M, K, N, N, true, false, 0) != 0) return -1;
             break;
           }
           case Op::ActGrad: {
@@ -1187,6 +1210,45 @@ int nsh_op_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, 
   return 0;
 }
 
+static GemmArgs plain_gemm(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, int64_t ldc, int act) {
+  GemmArgs g;
+  g.A = A; g.B = B; g.C = C;
+  g.M = (int)M; g.N = (int)N; g.K = (int)K;
+  g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+  g.act = act;
+  return g;
+}
+
+static int split_of(int64_t M, int64_t N, int64_t K, int splits) {
+  if (splits > 0) return splits;
+  return gemm_split_count(plain_gemm(nullptr, nullptr, nullptr, M, N, K, 0, 0, 0, 0), 1);
+}
+
+size_t nsh_op_gemm_splitk_workspace(int64_t M, int64_t N, int64_t K, int splits) {
+  if (M <= 0 || N <= 0 || K < 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return 0;
+  const int sp = split_of(M, N, K, splits);
+  return gemm_split_workspace(plain_gemm(nullptr, nullptr, nullptr, M, N, K, 0, 0, 0, 0), 1, sp) * sizeof(float);
+}
+
+int nsh_op_gemm_splitk(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                       int64_t ldb, int64_t ldc, int transA, int transB, int act, int splits, void* workspace) {
+  if (!A || !B || !C || M < 0 || N < 0 || K < 0 || splits < 0 || M > INT32_MAX || N > INT32_MAX ||
+      K > INT32_MAX) {
+    set_error("gemm_splitk: bad arguments");
+    return -1;
+  }
+  const int sp = split_of(M, N, K, splits);
+  if (sp > 1 && !workspace) {
+    set_error("gemm_splitk: missing workspace");
+    return -1;
+  }
+  const GemmArgs g = plain_gemm(A, B, C, M, N, K, lda, ldb, ldc, act);
+  if (launch_gemm_split(g, transA != 0, transB != 0, 1, sp, (float*)workspace, nullptr) != 0) return -1;
+  NSH_CHECK(hipStreamSynchronize(nullptr));
+  return 0;
+}
+
 #define NSH_OP_DONE()                             \
   do {                                            \
     NSH_CHECK(hipStreamSynchronize(nullptr));     \
@@ -1249,7 +1311,7 @@ static int op_muon(float* w, const float* g, int64_t r, int64_t c, float le, flo
   MuonMat* d = (MuonMat*)base;
   NSH_CHECK(hipMemcpy(d, &mm, sizeof(mm), hipMemcpyHostToDevice));
   if (launch_muon_gather(d, 1, r * c, nullptr) != 0) return -1;
-  if (launch_mgs_steps(d, 1, mm.nblk, mm.C, nullptr) != 0) return -1;
+  if (launch_mgs(d, &mm, 1, nullptr) != 0) return -1;
   if (launch_muon_update(d, 1, r * c, nullptr) != 0) return -1;
   NSH_CHECK(hipStreamSynchronize(nullptr));
   return 0;
@@ -1266,7 +1328,6 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
   MuonMat* d = (MuonMat*)base;
   float* wsf = (float*)(base + 256 * (((size_t)n * sizeof(MuonMat) + 255) / 256));
   int64_t max_elems = 0;
-  int max_c = 0, total = 0;
   for (int i = 0; i < n; i++) {
     MuonMat mm;
     mm.w = w[i];
@@ -1283,10 +1344,8 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
     mm.decay = 0.01f * lr;
     mats.push_back(mm);
     max_elems = std::max(max_elems, r[i] * c[i]);
-    max_c = std::max(max_c, mm.C);
-    total += mm.nblk;
   }
-  if (muon_batch(d, mats, max_elems, max_c, total, nullptr) != 0) return -1;
+  if (muon_batch(d, mats, max_elems, nullptr) != 0) return -1;
   NSH_CHECK(hipStreamSynchronize(nullptr));
   return 0;
 }
@@ -1319,6 +1378,27 @@ int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, i
 int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
                          int64_t D, int64_t H) {
   if (launch_attention_fwd(Q, K, V, ctx, lse, S, D, H, D, nullptr) != 0) return -1;
+  NSH_OP_DONE();
+}
+
+// workspace: delta [H*S] (rounded up to 64 floats), then dS when stored.
+static size_t attn_delta_floats(int64_t S, int64_t H) { return (size_t)(ceil_div(S * H, 64) * 64); }
+
+size_t nsh_op_attention_bwd_workspace(int64_t S, int64_t D, int64_t H, int store_ds) {
+  if (S <= 0 || H <= 0 || D <= 0) return 0;
+  return (attn_delta_floats(S, H) + (store_ds ? attention_bwd_ds_floats(S, D, H) : 0)) * sizeof(float);
+}
+
+int nsh_op_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                         const float* lse, float* dQ, float* dK, float* dV, int64_t S, int64_t D, int64_t H,
+                         int store_ds, void* workspace) {
+  if (!Q || !K || !V || !O || !dO || !lse || !dQ || !dK || !dV || !workspace) {
+    set_error("attention_bwd: bad arguments");
+    return -1;
+  }
+  float* delta = (float*)workspace;
+  float* ds = store_ds && attention_bwd_ds_floats(S, D, H) ? delta + attn_delta_floats(S, H) : nullptr;
+  if (launch_attention_bwd(Q, K, V, O, dO, lse, delta, dQ, dK, dV, S, D, H, D, ds, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 

@@ -70,6 +70,10 @@ def lib():
             "nsh_profile_reset": (ci, [vp]),
             "nsh_profile_report": (ci, [vp, ctypes.c_char_p, sz]),
             "nsh_op_gemm": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, ci]),
+            "nsh_op_attention_bwd_workspace": (sz, [i64, i64, i64, ci]),
+            "nsh_op_attention_bwd": (ci, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, ci, vp]),
+            "nsh_op_gemm_splitk_workspace": (sz, [i64, i64, i64, ci]),
+            "nsh_op_gemm_splitk": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, ci, ci, vp]),
             "nsh_model_last_routing": (ci, [vp, vp, vp, vp, sz]),
             "nsh_train_step_device": (ci, [vp, vp, vp, sz, _f32p, cf]),
             "nsh_model_read_value": (ci, [vp, ctypes.c_char_p, vp, sz]),
@@ -294,6 +298,14 @@ def bundled_nets():
 def gemm(dA, dB, dC, M, N, K, lda, ldb, ldc, transA=False, transB=False, act=0):
     check(lib().nsh_op_gemm(dA.ptr, dB.ptr, dC.ptr, M, N, K, lda, ldb, ldc, int(transA), int(transB), act),
           "gemm")
+
+
+def gemm_splitk(dA, dB, dC, M, N, K, lda, ldb, ldc, transA=False, transB=False, act=0, splits=0):
+    """nsh_op_gemm_splitk with a workspace of its own (splits 0: heuristic)."""
+    nb = lib().nsh_op_gemm_splitk_workspace(M, N, K, splits)
+    ws = DeviceArray(max(1, (nb + 3) // 4))
+    check(lib().nsh_op_gemm_splitk(dA.ptr, dB.ptr, dC.ptr, M, N, K, lda, ldb, ldc, int(transA), int(transB), act,
+                                   splits, ws.ptr), "gemm_splitk")
 
 
 def _p(d):

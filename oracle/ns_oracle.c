@@ -814,10 +814,15 @@ EXPORT void or_moe_bwd(const float* dout, const float* x, const float* Wg, const
 /* optimizer                                                               */
 /* ---------------------------------------------------------------------- */
 
-/* Number of interleaved partial sums in the MGS dot products: 1 (default)
- * is the reference's order; 2..8 are test-only reorderings. */
+/* Summation order of the MGS dot products: 1 (default) is the reference's
+ * order; 2..8 sum as that many interleaved partial sums (k mod P); -2..-8 as
+ * that many contiguous blocks of k.  All but 1 are test-only reorderings. */
 static int g_mgs_partials = 1;
-EXPORT void or_set_mgs_partials(int p) { g_mgs_partials = (p < 1) ? 1 : (p > 8 ? 8 : p); }
+EXPORT void or_set_mgs_partials(int p) {
+    if (p < -8) p = -8;
+    if (p > 8) p = 8;
+    g_mgs_partials = (p >= -1 && p <= 1) ? 1 : p;
+}
 
 /* Modified Gram-Schmidt over columns (M >= N) or rows (M < N), in place;
  * ns_orthonom codegen.cpp:1617-1633.  Right-looking form: when column j is
@@ -843,8 +848,15 @@ EXPORT void or_orthonom(float* G, int64_t M, int64_t N) {
         for (int64_t c = j + 1; c < C; c++) {
             float* v = T + (size_t)c * R;
             float dot = 0.f;
-            if (g_mgs_partials <= 1) {
+            if (g_mgs_partials == 1) {
                 for (int64_t k = 0; k < R; k++) dot += q[k] * v[k];
+            } else if (g_mgs_partials < 0) {
+                /* Test-only: -P contiguous blocks of k, summed in order. */
+                float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                const int P = -g_mgs_partials;
+                const int64_t blk = (R + P - 1) / P;
+                for (int64_t k = 0; k < R; k++) part[k / blk] += q[k] * v[k];
+                for (int p = 0; p < P; p++) dot += part[p];
             } else {
                 /* Test-only: the same dot product as P interleaved partial
                  * sums, to measure how far a mere change of summation order

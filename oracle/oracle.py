@@ -45,7 +45,7 @@ def build_command():
 
 def set_mgs_partials(p):
     """Test-only: sum each MGS dot product as p interleaved partial sums
-    (1 = the reference's order)."""
+    (p > 1) or as -p contiguous blocks (p < -1); 1 = the reference's order."""
     lib().or_set_mgs_partials(int(p))
 
 

@@ -1,9 +1,10 @@
 """Add the reordering drift band to the training fixtures of tests/golden.
 
 For every fixture that holds a loss trajectory, rerun the same training with
-the oracle set to sum each modified-Gram-Schmidt dot product as P
-interleaved partial sums (P = 2, 3, 4, 8; otherwise identical to the
-reference) and store `band` = max over P of |losses_P - losses|.
+the oracle set to sum each modified-Gram-Schmidt dot product in another
+order -- P interleaved partial sums (P = 2..8) or P contiguous blocks
+(P = 2, 4, 8); otherwise identical to the reference -- and store `band` =
+max over these orders of |losses_P - losses|.
 Muon normalises the rounding noise of rank-deficient gradient directions
 (ns_orthonom's +1e-30 guard), so the reference's own trajectory moves this
 much under a mere change of summation order; a GPU implementation is held to
@@ -31,7 +32,7 @@ def update(path, **extra):
     np.savez_compressed(path, **d)
 
 
-PARTIALS = (2, 3, 4, 8)
+PARTIALS = (2, 3, 4, 5, 6, 7, 8, -2, -4, -8)
 
 
 def spread(run, ref):

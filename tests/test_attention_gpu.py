@@ -35,6 +35,50 @@ def test_attention_core_matches_float64(S, D, H):
     helpers.assert_close(ctx.to_host(), core_ref(Q, K, V, S, D, H).ravel(), f"attention S={S} D={D} H={H}")
 
 
+def core_bwd_ref(Q, K, V, dO, S, D, H):
+    """Gradient of the attention core in float64: per head, with P the
+    softmax of the scaled scores, dV = P^T dO, dS = P o (dO V^T - rowsum(dO o O)),
+    dQ = scale dS K, dK = scale dS^T Q."""
+    dk = D // H
+    sc = 1.0 / np.sqrt(np.float32(dk))
+    Qd, Kd, Vd, dOd = (a.reshape(S, D).astype(np.float64) for a in (Q, K, V, dO))
+    dQ, dK, dV = np.zeros((S, D)), np.zeros((S, D)), np.zeros((S, D))
+    for h in range(H):
+        sl = slice(h * dk, (h + 1) * dk)
+        s = Qd[:, sl] @ Kd[:, sl].T * sc
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        o = p @ Vd[:, sl]
+        dV[:, sl] = p.T @ dOd[:, sl]
+        ds = p * (dOd[:, sl] @ Vd[:, sl].T - (dOd[:, sl] * o).sum(1, keepdims=True))
+        dQ[:, sl] = ds @ Kd[:, sl] * sc
+        dK[:, sl] = ds.T @ Qd[:, sl] * sc
+    return dQ, dK, dV
+
+
+@pytest.mark.parametrize("S,D,H", [(64, 128, 2), (192, 128, 2), (100, 128, 2), (256, 64, 2), (130, 64, 2),
+                                   (90, 64, 8), (1024, 512, 8), (2048, 512, 8)])
+@pytest.mark.parametrize("store_ds", [0, 1])
+def test_attention_core_backward_matches_float64(S, D, H, store_ds):
+    """Flash backward (head size 32/64: key-parallel dK/dV pass, then dQ
+    either from the stored dS or from a query-parallel pass recomputing S and
+    dP) and the small-head kernels, vs the float64 gradient; |d| <=
+    1e-4 |ref| + 1e-5 max|ref| per output."""
+    print(f"attention backward S={S} D={D} H={H} store_ds={store_ds}", flush=True)
+    Q, K, V, dO = (synth.normal(S * 20 + i, S * D, 1.0) for i in range(4))
+    dQ_, dK_, dV_ = (DA(S * D) for _ in range(3))
+    gQ, gK, gV, gdO = (DA.from_host(a) for a in (Q, K, V, dO))
+    ctx, lse = DA(S * D), DA(S * H)
+    runtime.op("attention_fwd", gQ, gK, gV, ctx, lse, S, D, H)
+    nb = runtime.lib().nsh_op_attention_bwd_workspace(S, D, H, store_ds)
+    ws = DA(max(1, (nb + 3) // 4))
+    runtime.op("attention_bwd", gQ, gK, gV, ctx, gdO, lse, dQ_, dK_, dV_, S, D, H, store_ds, ws)
+    for name, got, ref in zip(("dQ", "dK", "dV"), (dQ_, dK_, dV_), core_bwd_ref(Q, K, V, dO, S, D, H)):
+        ref = ref.ravel()
+        helpers.assert_close(got.to_host(), ref, f"attention {name} S={S} D={D} H={H} ds={store_ds}",
+                             atol=1e-5 * float(np.abs(ref).max()), rtol=1e-4)
+
+
 def test_attention_layer_matches_oracle():
     """Whole layer x -> (QKV projections, core, output projection) through a
     network driver vs the oracle's ns_attention_fwd restatement."""

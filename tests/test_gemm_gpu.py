@@ -59,3 +59,25 @@ def test_gemm_strided_output_and_zero_k():
     gC = runtime.DeviceArray(M * N)
     runtime.gemm(gA, gB, gC, M, N, K, 4, 24, N, False, False, 3)  # sigmoid(0) = 0.5
     assert np.all(gC.to_host() == 0.5)
+
+
+@pytest.mark.parametrize("M,N,K,splits", [(64, 64, 4096, 0), (512, 512, 16384, 0), (130, 70, 3001, 5),
+                                          (256, 128, 2048, 32), (100, 200, 40, 3), (64, 64, 16, 4)])
+@pytest.mark.parametrize("variant", ["tn", "nt"])
+def test_gemm_split_k_matches_oracle(M, N, K, splits, variant):
+    """Split K (the weight-gradient path of training): fixed-order sum of the
+    chunk partials, same result as the one-pass product to fp32 tolerance."""
+    print(f"gemm split-k {variant} M={M} N={N} K={K} splits={splits}", flush=True)
+    A, B = operands(M, N, K, 900 + M + N + K + splits)
+    if variant == "tn":
+        At = np.ascontiguousarray(A.reshape(M, K).T).ravel()
+        ref = oracle.matmul_grad_w(At, B, K, M, N)
+        dA, dB, tA, tB, lda, ldb = At, B, True, False, M, N
+    else:
+        Bt = np.ascontiguousarray(B.reshape(K, N).T).ravel()
+        ref = oracle.matmul_grad_a(A, Bt, M, N, K)
+        dA, dB, tA, tB, lda, ldb = A, Bt, False, True, K, K
+    gA, gB = runtime.DeviceArray.from_host(dA), runtime.DeviceArray.from_host(dB)
+    gC = runtime.DeviceArray(M * N)
+    runtime.gemm_splitk(gA, gB, gC, M, N, K, lda, ldb, N, tA, tB, 0, splits)
+    helpers.assert_close(gC.to_host(), ref, f"gemm split {variant} {M}x{N}x{K}/{splits}")

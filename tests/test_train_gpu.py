@@ -10,8 +10,9 @@ rank-deficient direction into a unit vector (LayerNorm outputs and
 softmax-minus-one-hot rows sum to zero, small batches have low rank), so the
 reference's own trajectory moves under a mere change of summation order.
 Each fixture records that movement (`band`: the largest deviation of the
-reference restatement with its MGS dot products summed in 2, 3, 4 or 8
-interleaved partial sums, tests/golden/make_band.py); a loss at step t must
+reference restatement with its MGS dot products summed in ten other orders:
+2..8 interleaved partial sums, 2, 4 or 8 contiguous blocks,
+tests/golden/make_band.py); a loss at step t must
 be within 1e-3 + 2 * max(band[:t+1]) of the reference.  AdamW-only
 networks have band 0, i.e. plain 1e-3, and their weights are compared too."""
 import os
@@ -110,11 +111,20 @@ def test_100_step_loss_curve_matches_reference(curve):
     assert np.all(dev <= tol), (dev, tol)
 
 
-@pytest.mark.parametrize("name,rows", [("c5t", 40), ("mlpt", 17), ("c5s", 64), ("moet", 41), ("moet", 300)])
+@pytest.mark.parametrize("name,rows", [("c5t", 40), ("mlpt", 17), ("c5s", 64), ("c5s", 2048), ("c5h", 192),
+                                       ("c5h", 100), ("moet", 41), ("moet", 300)])
 def test_every_value_of_one_train_step_matches_oracle(name, rows):
     """Each intermediate and gradient of one training step (read back from
     the device by IR value name) against the oracle's value of the same
-    name; the weights after the optimizer last."""
+    name; the weights after the optimizer last.
+
+    A value passes at |d| <= 1e-5 + 1e-3 |ref|, or within 4x the movement
+    that a random 1-ulp perturbation of the weights causes in the reference
+    itself (its conditioning).  The second bound matters only where the
+    network amplifies rounding: at 2048 tokens the attention output is an
+    average over 2048 rows (rms 0.025) that LayerNorm rescales by ~40, so the
+    reference's own logits move by 1.2x the first bound under 1-ulp weight
+    noise."""
     ir = helpers.ir_text(name)
     net = oracle.Net(ir)
     seed = 400 + rows
@@ -124,6 +134,10 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     om = oracle.Model(net, w)
     rec = {}
     om.train_step(x, y, 0.02, rec)
+    rng = np.random.default_rng(seed)
+    wp = (w * (1 + np.float32(2.0 ** -23) * rng.choice(np.array([-1, 1], np.float32), w.size))).astype(np.float32)
+    rec_p = {}
+    oracle.Model(net, wp).train_step(x, y, 0.02, rec_p)
     model = runtime.Model(runtime.Plan(ir), w)
     model.train_step(x, y, 0.02)
     bad = []
@@ -134,9 +148,10 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
         ref = rec["buf"][v]
         got = model.read_value(v, ref.size)
         viol = helpers.violation(got, ref, atol=1e-5, rtol=1e-3)
-        print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g}")
-        if viol > 1:
-            bad.append((ins.op, v, viol))
+        floor = helpers.violation(rec_p["buf"][v], ref, atol=1e-5, rtol=1e-3)
+        print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g} (1-ulp weight noise: x{floor:.3g})")
+        if viol > max(1.0, 4.0 * floor):
+            bad.append((ins.op, v, viol, floor))
     # Weights after the optimizer.  AdamW: the whole update.  Muon: the update
     # is lr*sqrt(min(r,c))*Q + 0.01*lr*W with Q = MGS(grad); only the Q
     # vectors of the determined prefix (rank of the gradient's vector set)
