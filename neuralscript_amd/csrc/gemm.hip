@@ -144,7 +144,7 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
 template <bool TA, bool TB, bool VEC>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g) {
+__global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
   const int M = g.M, N = g.N, K = g.K;
   const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
