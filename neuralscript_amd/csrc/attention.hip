@@ -317,7 +317,7 @@ struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
 // STORE_DS: also write dS = P o (dP - delta) (unscaled) to dS[h][query][key]
 // for flash_bwd_dq_ds_kernel; requires S % 64 == 0.
 template <int DK, bool STORE_DS>
-__global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                              const float* __restrict__ V, const float* __restrict__ dO,
                                                              const float* __restrict__ lse,
                                                              const float* __restrict__ delta, float* __restrict__ dK,
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __rest
     const float* gs = qs + 64 * Tile::P;
     const float* ls = qs + 2 * 64 * Tile::P;
     const float* ds = ls + 64;
-#pragma unroll
+#pragma unroll 1
     for (int qb = 0; qb < 2; qb++) {
       floatx16 sc, dp;
 #pragma unroll
@@ -392,9 +392,17 @@ __global__ __launch_bounds__(256) void flash_bwd_dkdv_kernel(const float* __rest
       if (STORE_DS && key < S) {
         // lanes 0-31 / 32-63 write 32 consecutive keys of one query row each;
         // every query row of the tile exists (S % 64 == 0)
+        // element v sits in row 8 (v / 4) + v % 4: walk a single pointer
         float* __restrict__ dst = dS + ((int64_t)h * S + it * 64 + qb * 32 + 4 * kh) * S + key;
 #pragma unroll
-        for (int v = 0; v < 16; v++) dst[(int64_t)(8 * (v >> 2) + (v & 3)) * S] = dp[v];
+        for (int g = 0; g < 4; g++) {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            *dst = dp[4 * g + j];
+            dst += S;
+          }
+          dst += 4 * (int64_t)S;
+        }
       }
       // dV += P^T dO, dK += dS^T Q: step s pairs query 8(s/4) + 4kh + s%4.
 #pragma unroll
