@@ -78,15 +78,72 @@ struct KVTile {
   }
 };
 
+// One K or V tile (64 keys x DK) in registers on its way to LDS (row pitch
+// DK + 4); rows past the end load a clamped row and are zeroed.
+template <int DK>
+struct HalfTile {
+  static constexpr int P = DK + 4;
+  static constexpr int kPer = kBK * DK / 4 / 256;
+  float4 r[kPer];
+  __device__ void load(const float* __restrict__ X, int64_t ld, int hcol, int key0, int S, int t) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
+      const int gk = key0 + key;
+      const bool in = gk < S;
+      const int64_t row = in ? gk : S - 1;
+      r[i] = keep4(in, *reinterpret_cast<const float4*>(X + row * ld + hcol + c));
+    }
+  }
+  __device__ void store(float* __restrict__ xs, int t) const {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<float4*>(xs + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = r[i];
+    }
+  }
+};
+
+// S^T tile (64 keys x this wave's 32 queries) = K_tile Q^T, in log2 units
+// (Q is pre-scaled by scale * log2(e)).
+template <int DK>
+__device__ __forceinline__ void score_tile(const float* __restrict__ ks, const float (&qf)[DK / 2], int l32, int kh,
+                                           floatx16 (&sc)[2]) {
+  constexpr int P = DK + 4;
+#pragma unroll
+  for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+    for (int v = 0; v < 16; v++) sc[kb][v] = 0.f;
+#pragma unroll
+  for (int g = 0; g < DK / 8; g++)
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      const float4 kv = *reinterpret_cast<const float4*>(ks + (kb * 32 + l32) * P + 8 * g + 4 * kh);
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * g + 0], sc[kb], 0, 0, 0);
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * g + 1], sc[kb], 0, 0, 0);
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * g + 2], sc[kb], 0, 0, 0);
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * g + 3], sc[kb], 0, 0, 0);
+    }
+}
+
+// Software-pipelined over key tiles: iteration `it` issues the score MFMAs
+// of tile it+1 alongside the softmax of tile it, then O^T += V_it^T P_it^T.
+// LDS holds two K tiles (it+1 in use, the other free for it+2) and two V
+// tiles (it in use, the other free for it+1).  The rescale of O by
+// exp2(m_old - m_new) is skipped when no lane's running max moved (the factor
+// would be exactly 1).
 template <int DK>
 __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                         const float* __restrict__ V, float* __restrict__ ctx,
                                                         float* __restrict__ lse, int S, int H, int64_t ld,
                                                         float scale_log2, int nqb) {
-  using Tile = KVTile<DK>;
-  constexpr int NS = DK / 2;    // MFMA steps of the score product
+  constexpr int P = DK + 4;
+  constexpr int TF = kBK * P;   // floats of one K or V tile in LDS
   constexpr int NDB = DK / 32;  // 32-wide head-dim blocks of the output
-  __shared__ __attribute__((aligned(16))) float sm[2 * 2 * Tile::kFloats];
+  __shared__ __attribute__((aligned(16))) float sm[4 * TF];
+  float* const kbuf = sm;           // K tile i at kbuf + (i & 1) * TF
+  float* const vbuf = sm + 2 * TF;  // V tile i at vbuf + (i & 1) * TF
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
@@ -95,13 +152,14 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
   const int hcol = h * DK;
   const int qrow = q0 + w * 32 + l32;
 
-  // B operand of S^T = K Q^T: this lane's query, head dims 8g + 4kh + (0..3).
-  float qf[NS];
+  // B operand of S^T = K Q^T: this lane's query (pre-scaled), head dims 8g + 4kh + (0..3).
+  float qf[DK / 2];
 #pragma unroll
   for (int g = 0; g < DK / 8; g++) {
     const int64_t row = qrow < S ? qrow : S - 1;
     const float4 x = keep4(qrow < S, *reinterpret_cast<const float4*>(Q + row * ld + hcol + 8 * g + 4 * kh));
-    qf[4 * g] = x.x; qf[4 * g + 1] = x.y; qf[4 * g + 2] = x.z; qf[4 * g + 3] = x.w;
+    qf[4 * g] = x.x * scale_log2; qf[4 * g + 1] = x.y * scale_log2;
+    qf[4 * g + 2] = x.z * scale_log2; qf[4 * g + 3] = x.w * scale_log2;
   }
 
   floatx16 o[NDB];
@@ -111,50 +169,51 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
     for (int v = 0; v < 16; v++) o[d][v] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  Tile tile;
   const int nkv = (S + kBK - 1) / kBK;
-  tile.load(K, V, ld, hcol, 0, S, t);
-  tile.store(sm, t);
+  HalfTile<DK> tk, tv;
+  tk.load(K, ld, hcol, 0, S, t);
+  tv.load(V, ld, hcol, 0, S, t);
+  tk.store(kbuf, t);
+  tv.store(vbuf, t);
+  tk.load(K, ld, hcol, (nkv > 1 ? 1 : 0) * kBK, S, t);
+  tk.store(kbuf + TF, t);
   __syncthreads();
+  floatx16 sc[2], sn[2];
+  score_tile<DK>(kbuf, qf, l32, kh, sc);
+  __syncthreads();  // kbuf tile 0 is overwritten at the end of iteration 0
 
   for (int it = 0; it < nkv; it++) {
-    const int cur = it & 1;
-    const bool more = it + 1 < nkv;
-    if (more) tile.load(K, V, ld, hcol, (it + 1) * kBK, S, t);
-    const float* ks = sm + cur * 2 * Tile::kFloats;
-    const float* vs = ks + Tile::kFloats;
-
-    floatx16 sc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) sc[kb][v] = 0.f;
-#pragma unroll
-    for (int g = 0; g < DK / 8; g++)
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++) {
-        const float4 kv = *reinterpret_cast<const float4*>(ks + (kb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qf[4 * g + 0], sc[kb], 0, 0, 0);
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qf[4 * g + 1], sc[kb], 0, 0, 0);
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qf[4 * g + 2], sc[kb], 0, 0, 0);
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qf[4 * g + 3], sc[kb], 0, 0, 0);
-      }
+    // prefetch K tile it+2 and V tile it+1 (clamped: the last tiles reload)
+    tk.load(K, ld, hcol, min(it + 2, nkv - 1) * kBK, S, t);
+    tv.load(V, ld, hcol, min(it + 1, nkv - 1) * kBK, S, t);
+    if (it + 1 < nkv) score_tile<DK>(kbuf + ((it + 1) & 1) * TF, qf, l32, kh, sn);
 
     // Online softmax for this lane's query (keys 8*(v/4) + 4kh + v%4 of each block).
     const int kbase = it * kBK;
+    if (kbase + kBK > S) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int key = kbase + kb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
+          if (key >= S) sc[kb][v] = -INFINITY;
+        }
+    }
     float mloc = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int key = kbase + kb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        const float x = key < S ? sc[kb][v] * scale_log2 : -INFINITY;
-        sc[kb][v] = x;
-        mloc = fmaxf(mloc, x);
-      }
+      for (int v = 0; v < 16; v++) mloc = fmaxf(mloc, sc[kb][v]);
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     const float mnew = fmaxf(m, mloc);
-    const float corr = exp2f(m - mnew);
+    if (__any(mnew > m)) {
+      const float corr = exp2f(m - mnew);
+      l *= corr;
+#pragma unroll
+      for (int d = 0; d < NDB; d++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[d][v] *= corr;
+    }
     float lsum = 0.f;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
@@ -165,14 +224,11 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
         lsum += p;
       }
     lsum += __shfl_xor(lsum, 32, 64);
-    l = l * corr + lsum;
+    l += lsum;
     m = mnew;
-#pragma unroll
-    for (int d = 0; d < NDB; d++)
-#pragma unroll
-      for (int v = 0; v < 16; v++) o[d][v] *= corr;
 
     // O^T += V^T P^T: step s of key block kb pairs key 8*(s/4)+4kh+s%4.
+    const float* vs = vbuf + (it & 1) * TF;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -180,11 +236,16 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
         const int key = kb * 32 + 8 * (s >> 2) + 4 * kh + (s & 3);
 #pragma unroll
         for (int d = 0; d < NDB; d++)
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * Tile::P + d * 32 + l32], sc[kb][s], o[d], 0, 0, 0);
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * P + d * 32 + l32], sc[kb][s], o[d], 0, 0, 0);
       }
 
-    if (more) tile.store(sm + (cur ^ 1) * 2 * Tile::kFloats, t);
+    // K tile it (consumed last iteration) and V tile it-1 (consumed last
+    // iteration) are free: fill them with K tile it+2 and V tile it+1.
+    tk.store(kbuf + (it & 1) * TF, t);
+    tv.store(vbuf + ((it + 1) & 1) * TF, t);
     __syncthreads();
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) sc[kb] = sn[kb];
   }
 
   // Row statistics for the backward pass: log2-sum-exp of the scaled scores.
