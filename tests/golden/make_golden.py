@@ -9,7 +9,9 @@ weight blob.  Inputs are not stored; they are regenerated from the seeds
 (SplitMix64, neuralscript_amd/synth.py) and checked against a stored digest.
 
 Run in the build container (needs /root/reference built by oracle/Makefile):
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [net ...]    (default: every net)
+then tests/golden/make_band.py, which adds the reordering band to the
+training fixtures.
 """
 import hashlib
 import os
@@ -40,6 +42,7 @@ CASES = [
     ("c5t", 33, 108, 3, 0.01, False),
     ("moet", 41, 109, 3, 0.01, False),
     ("c5s", 64, 110, 2, 0.003, False),
+    ("moeb", 300, 111, 3, 0.01, False),
 ]
 
 
@@ -55,7 +58,7 @@ def case_inputs(name, rows, seed):
 # 100-step loss curves, host-side cosine warmup schedule (lr * lr_scale(t),
 # t = 0..99, so the first step has lr 0), on reduced c5 twins:
 # name, tokens, seed, base lr
-CURVES = [("c5s", 256, 201, 3e-4), ("c5s", 256, 202, 0.02), ("c5t", 96, 203, 0.05)]
+CURVES = [("c5s", 256, 201, 3e-4), ("c5s", 256, 202, 0.02), ("c5t", 96, 203, 0.05), ("moeb", 512, 204, 0.01)]
 
 
 def curve_lrs(base, steps=100):
@@ -66,8 +69,10 @@ def digest(a):
     return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()[:16]
 
 
-def main():
+def main(names=()):
     for name, rows, seed, steps, lr, life in CASES:
+        if names and name not in names:
+            continue
         net, x, y = case_inputs(name, rows, seed)
         w = helpers.net_weights(name, seed)
         lib = NsLib(os.path.join(helpers.REF, f"lib{name}.so"))
@@ -95,8 +100,10 @@ def main():
         print(name, {k: getattr(v, "shape", None) for k, v in rec.items()})
 
 
-def curves():
+def curves(names=()):
     for name, rows, seed, base in CURVES:
+        if names and name not in names:
+            continue
         net = oracle.Net(helpers.ir_text(name))
         x = helpers.net_inputs(net, name, seed, rows)
         y = helpers.net_labels(net, seed, rows)
@@ -113,5 +120,5 @@ def curves():
 
 
 if __name__ == "__main__":
-    main()
-    curves()
+    main(sys.argv[1:])
+    curves(sys.argv[1:])

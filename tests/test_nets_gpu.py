@@ -12,7 +12,7 @@ from neuralscript_amd import runtime, workloads
 
 pytestmark = pytest.mark.gpu
 
-FWD_NETS = ["c1", "c2s", "xor", "mlpt", "c3s", "c4s", "c4k", "c5t", "moet", "c5s"]
+FWD_NETS = ["c1", "c2s", "xor", "mlpt", "c3s", "c4s", "c4k", "c5t", "moet", "c5s", "moeb"]
 
 
 def golden(name):
