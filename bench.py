@@ -13,6 +13,10 @@ Prints ONE JSON line with the driver's contract plus
                   emits, built from its sources into oracle/_ref) on a bounded
                   sample of the same workload, 1 core; the oracle port when
                   that build is absent.
+--config c3 | c4 (forward) and c5 (training step) time the other configs the
+same way (device-resident inputs) and report a per-region breakdown and the
+roofline of their dominant kernel; c4 adds the realised expert histogram and
+the top-2 gate-logit ties.
 """
 from __future__ import annotations
 
@@ -91,7 +95,36 @@ def c3_work(M=16384, D=1024, H=16, V=32000):
 
 
 def c4_work(M=65536, D=1024, E=64, H=1024):
-    return {"moe": 2.0 * M * D * E + 4.0 * M * D * H}
+    return {"moe_route": 2.0 * M * D * E, "moe_experts": 4.0 * M * D * H}
+
+
+# Dominant kernel of each --config run: (profile region, kernel, bound).
+DOMINANT = {"c3": ("attention_fwd", "flash_fwd_kernel<64>", "mfma"),
+            "c4": ("moe_experts", "gemm_f32_kernel (grouped by expert, gather/scatter rows)", "mfma"),
+            "c5": ("attention_bwd", "flash_bwd_dkdv_kernel<64,true> + flash_bwd_dq_ds_kernel<64>", "mfma")}
+
+
+def roofline_of(key, region, work, ms_per_call):
+    """Roofline object of the dominant kernel: algorithmic FLOP of one call
+    over the HIP-event time of that call (profile region on the model's
+    stream); traffic not measured for these configs."""
+    _, kernel, bound = DOMINANT[key]
+    achieved = work / (ms_per_call * 1e-3) / 1e12
+    return {"bound": bound, "kernel": kernel, "region": region, "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "flop_per_launch": work,
+            "avg_launch_ms": ms_per_call, "traffic": None}
+
+
+def routing_report(best, logits, E):
+    """Realised expert histogram and top-2 gate-logit ties (exact, and within
+    1e-6 relative) of the last routed batch."""
+    hist = np.bincount(best[best >= 0], minlength=E)
+    lg = logits.reshape(-1, E).astype(np.float64)
+    top2 = np.sort(lg, axis=1)[:, -2:]
+    gap = top2[:, 1] - top2[:, 0]
+    return {"histogram": hist.tolist(), "max_share": float(hist.max() / max(1, hist.sum())),
+            "exact_ties": int((gap == 0).sum()),
+            "near_ties_1e-6": int(((gap > 0) & (gap <= 1e-6 * np.maximum(1.0, np.abs(top2[:, 1])))).sum())}
 
 
 def bench_forward(key, steps, warmup):
@@ -117,6 +150,11 @@ def bench_forward(key, steps, warmup):
     model.sync()
     dt = time.perf_counter() - t0
     prof = model.profile_report()
+    routing = None
+    if key == "c4":
+        E = workloads.ir_shapes(plan.ir)["moe_g_w"][1]
+        best, _, lg = model.last_routing(wl.rows, E)
+        routing = routing_report(best, lg, E)
     model.free()
     work = {"c3": c3_work, "c4": c4_work}.get(key, lambda: {})()
     kernels = {}
@@ -129,17 +167,24 @@ def bench_forward(key, steps, warmup):
             else:
                 e["TFLOP/s"] = work[k] / (ms * 1e-3) / 1e12
         kernels[k] = e
-    return {"metric": METRIC, "value": wl.rows * steps / dt, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-            "warmup": warmup, "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device"},
-            "kernels": kernels}
+    region = DOMINANT[key][0]
+    out = {"metric": METRIC, "value": wl.rows * steps / dt, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device"},
+           "roofline": roofline_of(key, region, work[region],
+                                   prof[region]["ms"] / prof[region]["calls"]),
+           "kernels": kernels}
+    if routing is not None:
+        out["routing"] = routing
+    return out
 
 
 def c5_work(M=16384, D=512, H=8, V=8192, FF=2048, C=8192):
     """Algorithmic FLOP of one c5 training step (attention counted once)."""
     dense_fwd = 2.0 * M * (4 * D * D + D * FF + FF * D + D * C)
-    return {"dense": 3 * dense_fwd, "attention": 4.0 * M * M * D * 3, "total": 3 * dense_fwd + 12.0 * M * M * D}
+    return {"dense": 3 * dense_fwd, "attention": 4.0 * M * M * D * 3, "attention_bwd": 8.0 * M * M * D,
+            "total": 3 * dense_fwd + 12.0 * M * M * D}
 
 
 def bench_train(key, steps, warmup):
@@ -173,11 +218,14 @@ def bench_train(key, steps, warmup):
     model.free()
     work = c5_work()
     kernels = {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["calls"] / steps} for k, v in prof.items()}
+    att = prof["attention_bwd"]
     return {"metric": METRIC, "value": steps / dt, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
             "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "f32", "data": "synthetic",
             "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device"},
-            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss), "kernels": kernels}
+            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
+            "roofline": roofline_of(key, "attention_bwd", work["attention_bwd"], att["ms"] / att["calls"]),
+            "kernels": kernels}
 
 
 def bench_c2(steps, warmup, with_cpu):

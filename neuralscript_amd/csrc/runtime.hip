@@ -337,9 +337,12 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       MoeWork w;
       if (moe_work(m, M, &w) != 0) return -1;
       if (train && !(w.pre = scratch(m, "moe_pre", (size_t)(M * q.H)))) return -1;
-      Prof p(m, "moe");
-      if (launch_moe_route(fr.ptr[I.in[0]], fr.ptr[I.in[1]], m->d_active, w, M, q.D, q.E, s) != 0) return -1;
+      {
+        Prof p(m, "moe_route");  // router logits, expert choice, stable dispatch
+        if (launch_moe_route(fr.ptr[I.in[0]], fr.ptr[I.in[1]], m->d_active, w, M, q.D, q.E, s) != 0) return -1;
+      }
       m->moe_last_m = M;
+      Prof p(m, "moe_experts");  // the two grouped expert GEMMs
       return launch_moe_experts(fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]], w, out, M, q.D, q.H, q.E, s);
     }
     case Op::Dropout:
