@@ -106,6 +106,100 @@ __global__ __launch_bounds__(256) void moe_router_kernel(const float* __restrict
   }
 }
 
+// Router with one lane per token: a workgroup holds 64 tokens, and each of
+// its 4 waves accumulates EG = E/4 experts of all 64 tokens in registers
+// (E <= 64, D % 4 == 0, 16-byte aligned x).  The gate weights a wave needs
+// are wave-uniform, so they come through scalar loads and feed the
+// multiplies as scalar operands: two vector instructions per multiply-add,
+// the unfused sequential-k arithmetic of the reference.  x goes through LDS
+// in coalesced 32-wide k slabs (register prefetch of the next slab); the
+// logits meet in LDS for the routing of each token by wave 0.
+constexpr int kRT = 64;       // tokens per workgroup (one per lane)
+constexpr int kRK = 32;       // k slab
+constexpr int kRP = kRK + 4;  // LDS row pitch of the x slab
+
+template <int EG, bool EXACT>  // EXACT: E == 4 * EG (no per-expert guards)
+__global__ __launch_bounds__(256) void moe_router_tok_kernel(const float* __restrict__ x, const float* __restrict__ Wg,
+                                                             const uint8_t* __restrict__ active,
+                                                             float* __restrict__ logits, int* __restrict__ best,
+                                                             float* __restrict__ prob, int M, int D, int E) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float xs[kRT * kRP];
+  __shared__ float lg[kRT][4 * EG + 1];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform, so weights load as scalars
+  const int tok0 = blockIdx.x * kRT;
+  const int e0 = wv * EG;  // first expert of this wave
+  float acc[EG];
+#pragma unroll
+  for (int j = 0; j < EG; j++) acc[j] = 0.f;
+  // slab staging: float4 i of thread t is token (t + 256 i) / 8, k offset 4 ((t + 256 i) % 8)
+  float4 st[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int f = t + 256 * i, r = f >> 3, c = (f & 7) * 4;
+    st[i] = (tok0 + r < M && c < D) ? *reinterpret_cast<const float4*>(x + (int64_t)(tok0 + r) * D + c)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int k0 = 0; k0 < D; k0 += kRK) {
+    __syncthreads();  // previous slab consumed
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int f = t + 256 * i, r = f >> 3, c = (f & 7) * 4;
+      *reinterpret_cast<float4*>(xs + r * kRP + c) = st[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int f = t + 256 * i, r = f >> 3, c = (f & 7) * 4;
+      const int k = k0 + kRK + c;
+      st[i] = (tok0 + r < M && k < D) ? *reinterpret_cast<const float4*>(x + (int64_t)(tok0 + r) * D + k)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int kn = min(kRK, D - k0);  // a multiple of 4
+    for (int kq = 0; kq < kn; kq += 4) {
+      const float4 xv = *reinterpret_cast<const float4*>(xs + lane * kRP + kq);
+      const float xk[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const float* __restrict__ wr = Wg + (int64_t)(k0 + kq + u) * (EXACT ? 4 * EG : E) + e0;
+#pragma unroll
+        for (int j = 0; j < EG; j++)
+          if (EXACT || e0 + j < E) {
+            const float prod = xk[u] * wr[j];
+            acc[j] = acc[j] + prod;
+          }
+      }
+    }
+  }
+  const int tok = tok0 + lane;
+#pragma unroll
+  for (int j = 0; j < EG; j++) {
+    lg[lane][e0 + j] = acc[j];
+    if (logits && tok < M && (EXACT || e0 + j < E)) logits[(int64_t)tok * E + e0 + j] = acc[j];
+  }
+  __syncthreads();
+  if (wv != 0 || tok >= M) return;
+  // Routing, experts in ascending order (first strict maximum wins).
+  const float* l = lg[lane];
+  float mx = -1.0e30f;
+  for (int e = 0; e < E; e++)
+    if ((!active || active[e]) && l[e] > mx) mx = l[e];
+  float sum = 0.f, bv = 0.f;
+  int b = -1;
+  for (int e = 0; e < E; e++) {
+    if (active && !active[e]) continue;
+    const float v = exp_rn(l[e] - mx);
+    sum = sum + v;
+    if (b < 0 || v > bv) {
+      b = e;
+      bv = v;
+    }
+  }
+  best[tok] = b;
+  prob[tok] = (sum > 0.f && b >= 0) ? bv / sum : 0.f;
+}
+
 // In-block rank of each token among same-expert tokens, and block counts.
 __global__ __launch_bounds__(kBlk) void moe_rank_kernel(const int* __restrict__ best, int* __restrict__ rank,
                                                         int* __restrict__ bcount, int M, int E) {
@@ -122,6 +216,53 @@ __global__ __launch_bounds__(kBlk) void moe_rank_kernel(const int* __restrict__ 
     for (int j = 0; j < kBlk; j++) c += b[j] == e;
     bcount[(int64_t)blockIdx.x * E + e] = c;
   }
+}
+
+// moe_scan_kernel with the block counts staged in LDS (nblk * E <= 16384):
+// coalesced loads, column sums from LDS, coalesced offset stores.
+constexpr int kScanLds = 16384;
+__global__ __launch_bounds__(256) void moe_scan_lds_kernel(int* __restrict__ bcount, int* __restrict__ seg,
+                                                           int* __restrict__ tiles, int* __restrict__ ntiles,
+                                                           int nblk, int E, int bm) {
+  __shared__ int cnt[kScanLds];
+  __shared__ int base[257], tb[257];
+  const int t = threadIdx.x;
+  const int n = nblk * E;
+  for (int i = t; i < n; i += 256) cnt[i] = bcount[i];
+  __syncthreads();
+  if (t < E) {
+    int c = 0;
+    for (int k = 0; k < nblk; k++) c += cnt[k * E + t];
+    base[t + 1] = c;  // total of expert t, turned into the prefix below
+  }
+  __syncthreads();
+  if (t == 0) {
+    base[0] = 0;
+    tb[0] = 0;
+    for (int e = 0; e < E; e++) {
+      const int tot = base[e + 1];
+      base[e + 1] = base[e] + tot;
+      tb[e + 1] = tb[e] + (tot + bm - 1) / bm;
+    }
+    *ntiles = tb[E];
+    seg[E] = base[E];
+  }
+  __syncthreads();
+  if (t < E) {
+    seg[t] = base[t];
+    int run = base[t];
+    for (int k = 0; k < nblk; k++) {
+      const int c = cnt[k * E + t];
+      cnt[k * E + t] = run;
+      run += c;
+    }
+    for (int i = 0; i < tb[t + 1] - tb[t]; i++) {
+      tiles[2 * (tb[t] + i)] = t;
+      tiles[2 * (tb[t] + i) + 1] = i;
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += 256) bcount[i] = cnt[i];
 }
 
 // Expert segments, per-block offsets (in place over bcount) and the
@@ -181,10 +322,11 @@ __global__ void gelu_rows_kernel(const float* __restrict__ pre, float* __restric
   hid[i] = act_apply(pre[i], kActGeluMoe);
 }
 
+// Rows of tokens routed nowhere (no live expert) are zero; one thread per token.
 __global__ void zero_rows_kernel(const int* __restrict__ best, float* __restrict__ out, int M, int D) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * D) return;
-  if (best[i / D] < 0) out[i] = 0.f;
+  const int tok = blockIdx.x * blockDim.x + threadIdx.x;
+  if (tok >= M || best[tok] >= 0) return;
+  for (int c = 0; c < D; c++) out[(int64_t)tok * D + c] = 0.f;
 }
 
 }  // namespace
@@ -202,16 +344,36 @@ int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, con
     set_error("moe: more than 256 experts or too many tokens");
     return -1;
   }
-  const dim3 g1((unsigned)ceil_div(M, kTok));
   const int m = (int)M, d = (int)D, e = (int)E;
-  if (E <= 64) hipLaunchKernelGGL(moe_router_kernel<1>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
-  else if (E <= 128) hipLaunchKernelGGL(moe_router_kernel<2>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
-  else hipLaunchKernelGGL(moe_router_kernel<4>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+  const bool tok_path = E <= 64 && D % 4 == 0 && ((uintptr_t)x & 15) == 0;
+  if (tok_path) {
+    const dim3 g((unsigned)ceil_div(M, kRT));
+#define NSH_ROUTER(EG_)                                                                                      \
+  if (E == 4 * EG_)                                                                                          \
+    hipLaunchKernelGGL((moe_router_tok_kernel<EG_, true>), g, dim3(256), 0, s, x, Wg, active, w.logits, w.best, \
+                       w.prob, m, d, e);                                                                     \
+  else                                                                                                       \
+    hipLaunchKernelGGL((moe_router_tok_kernel<EG_, false>), g, dim3(256), 0, s, x, Wg, active, w.logits,       \
+                       w.best, w.prob, m, d, e)
+    if (E <= 8) { NSH_ROUTER(2); }
+    else if (E <= 16) { NSH_ROUTER(4); }
+    else if (E <= 32) { NSH_ROUTER(8); }
+    else { NSH_ROUTER(16); }
+#undef NSH_ROUTER
+  } else {
+    const dim3 g1((unsigned)ceil_div(M, kTok));
+    if (E <= 64) hipLaunchKernelGGL(moe_router_kernel<1>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+    else if (E <= 128) hipLaunchKernelGGL(moe_router_kernel<2>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+    else hipLaunchKernelGGL(moe_router_kernel<4>, g1, dim3(256), 0, s, x, Wg, active, w.logits, w.best, w.prob, m, d, e);
+  }
   NSH_LAUNCHED();
   const int nblk = (int)ceil_div(M, kBlk);
   hipLaunchKernelGGL(moe_rank_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, m, e);
   NSH_LAUNCHED();
-  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
+  if ((int64_t)nblk * E <= kScanLds)
+    hipLaunchKernelGGL(moe_scan_lds_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
+  else
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
   NSH_LAUNCHED();
   hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, w.perm, m, e);
   NSH_LAUNCHED();
@@ -250,7 +412,7 @@ int launch_moe_experts(const float* x, const float* We1, const float* We2, const
   g2.sBg = H * D;
   if (launch_gemm_ex(g2, false, false, 1, s) != 0) return -1;
   // tokens without a live expert
-  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)ceil_div(M * D, 256)), dim3(256), 0, s, w.best, out, (int)M,
+  hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, w.best, out, (int)M,
                      (int)D);
   NSH_LAUNCHED();
   return 0;
