@@ -109,6 +109,21 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
 int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s);
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 
+// movement.hip -------------------------------------------------------------------
+int launch_binop(const float* A, const float* B, float* C, int64_t na, int64_t nb, int code, hipStream_t s);
+// out = in, then softmax over each full row of `last` (a tail shorter than a row is copied)
+int launch_softmax(const float* in, float* out, int64_t n, int64_t last, hipStream_t s);
+int launch_transpose(const float* in, float* out, int64_t R, int64_t C, hipStream_t s);
+int launch_concat_cols(const float* a, const float* b, float* out, int64_t R, int64_t ca, int64_t cb, hipStream_t s);
+int launch_slice_cols(const float* in, float* out, int64_t M, int64_t C, int64_t start, int64_t width,
+                      hipStream_t s);
+int launch_index(const float* in, const int64_t* idx, float* out, int64_t M, int64_t C, int64_t L, int axis,
+                 hipStream_t s);
+int launch_scatter(const float* in, const int64_t* idx, const float* upd, float* out, int64_t R, int64_t C,
+                   int64_t L, int axis, hipStream_t s);
+int launch_fill(float* out, int64_t n, float v, hipStream_t s);
+int launch_copy(const float* in, float* out, int64_t n, hipStream_t s);
+
 // moe.hip ----------------------------------------------------------------------
 struct MoeWork {
   float* logits;   // [M, E]  raw router logits (kept for tie reports)

@@ -50,6 +50,25 @@ int64_t comment_int(const std::string& c, const std::string& key) {
   return -1;
 }
 
+// VALUE of a key=VALUE token (whitespace-delimited) in a comment, or "".
+std::string comment_str(const std::string& c, const std::string& key) {
+  size_t p = 0;
+  while ((p = c.find(key + "=", p)) != std::string::npos) {
+    if (p == 0 || std::isspace((unsigned char)c[p - 1])) {
+      size_t e = p + key.size() + 1;
+      size_t f = e;
+      while (f < c.size() && !std::isspace((unsigned char)c[f])) f++;
+      return c.substr(e, f - e);
+    }
+    p += key.size();
+  }
+  return "";
+}
+
+bool is_fusible(Op op) {  // fusion.cpp:23-40
+  return op == Op::Act || op == Op::Softmax || op == Op::LayerNorm || op == Op::Binop;
+}
+
 struct Raw {
   std::string op, comment;
   std::vector<std::string> ids;
@@ -199,6 +218,48 @@ Plan* parse_plan(const char* text, std::string* err) {
       if (o == "ns.tensor.alloc") { I.op = Op::Alloc; }
       else if (o == "ns.grad" || o == "ns.forward") { I.op = Op::Marker; nres = 0; }
       else if (o == "ns.matmul") I.op = Op::Matmul;
+      else if (o == "ns.activation.softmax") I.op = Op::Softmax;
+      else if (o == "ns.subview_binop") {
+        I.op = Op::Binop;
+        const std::string b = comment_str(r.comment, "op");
+        I.binop = b == "-" ? 1 : b == "*" ? 2 : b == "/" ? 3 : 0;  // codegen.cpp:2010-2013
+      }
+      else if (o == "ns.constant") {
+        I.op = Op::Constant;
+        std::string v = comment_str(r.comment, "value");
+        if (v.empty()) {  // "constant <literal>"
+          const size_t sp = r.comment.rfind(' ');
+          v = sp == std::string::npos ? r.comment : r.comment.substr(sp + 1);
+        }
+        char* e = nullptr;
+        I.value = (float)std::strtod(v.c_str(), &e);
+        if (e == v.c_str()) { *err = "bad constant: " + r.comment; return false; }
+      }
+      else if (o == "ns.transpose") I.op = Op::Transpose;
+      else if (o == "ns.reshape") I.op = Op::Reshape;
+      else if (o == "ns.concat" || o == "ns.slice" || o == "ns.index" || o == "ns.scatter") {
+        I.op = o == "ns.concat" ? Op::Concat : o == "ns.slice" ? Op::Slice : o == "ns.index" ? Op::Index : Op::Scatter;
+        const std::string ax = comment_str(r.comment, "axis");
+        if (ax.empty()) { *err = o + " without its axis= attribute (use the attribute-preserving IR printer)"; return false; }
+        I.axis = std::atoi(ax.c_str());
+        if (I.op == Op::Concat) I.axis = ax == "0" ? 0 : 1;  // codegen.cpp:2105
+        if (I.op == Op::Slice) {
+          I.start = comment_int(r.comment, "start");
+          I.stop = comment_int(r.comment, "stop");
+          if (I.start < 0 || I.stop < I.start) { *err = "bad slice range: " + r.comment; return false; }
+        }
+        if (I.op == Op::Index || I.op == Op::Scatter) {
+          std::stringstream ls(comment_str(r.comment, "idx"));
+          std::string t;
+          while (std::getline(ls, t, ',')) {
+            if (t.empty()) continue;
+            char* e = nullptr;
+            const long long v = std::strtoll(t.c_str(), &e, 10);
+            if (*e != '\0') { *err = "bad index list: " + r.comment; return false; }
+            I.idx.push_back(v);
+          }
+        }
+      }
       else if (starts(o, "ns.activation.")) {
         I.op = Op::Act;
         I.act = act_code(o.substr(14));
@@ -250,11 +311,17 @@ Plan* parse_plan(const char* text, std::string* err) {
           {Op::MatmulGradA, 2}, {Op::MatmulGradW, 3}, {Op::ActGrad, 2}, {Op::LayerNormGrad, 2},
           {Op::EmbeddingGradW, 3}, {Op::AttnGradX, 6}, {Op::AttnGradWq, 6}, {Op::AttnGradWk, 6},
           {Op::AttnGradWv, 6}, {Op::AttnGradWo, 6}, {Op::MoeGradX, 5}, {Op::MoeGradWg, 5},
-          {Op::MoeGradWe1, 5}, {Op::MoeGradWe2, 5}};
+          {Op::MoeGradWe1, 5}, {Op::MoeGradWe2, 5}, {Op::Binop, 2}, {Op::Softmax, 1}, {Op::Transpose, 1},
+          {Op::Concat, 2}, {Op::Reshape, 1}, {Op::Slice, 1}, {Op::Index, 1}, {Op::Scatter, 2}};
       auto ar = arity.find(I.op);
       if (ar != arity.end() && I.in.size() < ar->second) { *err = "too few operands: " + o; return false; }
       if (I.op == Op::OptStep && I.in.size() % 2) { *err = "odd ns.opt.step operand list"; return false; }
       if (I.res >= 0 && r.has_type && r.dims.size() > 1) rtc(I.res) = r.dims[1];
+      if (I.res >= 0) {
+        if ((int)F->srows.size() <= I.res) { F->srows.resize(I.res + 1, -1); F->scols.resize(I.res + 1, -1); }
+        F->srows[I.res] = r.has_type && !r.dims.empty() ? r.dims[0] : -1;
+        F->scols[I.res] = r.has_type && r.dims.size() > 1 ? r.dims[1] : -1;
+      }
       I.rt_cols = I.res >= 0 ? rtc(I.res) : -1;
       if (I.op == Op::Attention) {
         const int64_t h = comment_int(r.comment, "heads");
@@ -293,8 +360,13 @@ Plan* parse_plan(const char* text, std::string* err) {
       }
       if (I.op == Op::ActGrad) {
         bool found = false;
-        for (auto& J : F->ins)
+        for (auto& J : F->ins) {
           if (J.op == Op::Act && J.in[0] == I.in[1]) { I.act = J.act; found = true; }
+          // softmax's gradient is emitted as ACTIVATION_GRAD "softmax", whose
+          // derivative code is 0, i.e. 1 (mlir_compiler.cpp:348-360,
+          // codegen.cpp:3074-3081, 1305-1315)
+          if (J.op == Op::Softmax && J.in[0] == I.in[1]) { I.act = 0; found = true; }
+        }
         if (!found) { *err = "activation grad without its forward"; return false; }
       }
     }
@@ -305,13 +377,81 @@ Plan* parse_plan(const char* text, std::string* err) {
       if (I.op == Op::Embedding) cand = I.in[1];
       else if (I.op == Op::Matmul) cand = I.in[0];
       else if (!F->train && (I.op == Op::Attention || I.op == Op::LayerNorm || I.op == Op::Moe ||
-                             I.op == Op::Dropout || I.op == Op::Act))
-        cand = I.in[0];
+                             I.op == Op::Dropout || I.op == Op::Act || I.op == Op::Softmax ||
+                             I.op == Op::Transpose || I.op == Op::Concat || I.op == Op::Reshape ||
+                             I.op == Op::Slice || I.op == Op::Index || I.op == Op::Scatter))
+        cand = I.in[0];  // codegen.cpp:44-61
       if (cand >= 0 && !is_w(cand)) { F->x = cand; break; }
     }
     for (auto& I : F->ins)
       if (I.op == Op::CrossEntropy) F->y = I.in[1];
     if (F->x < 0) { *err = "cannot find the runtime input of " + f.name; return false; }
+    // static shape table: weights, result types, and the input's width
+    // (first GEMM's K, else 1; codegen.cpp:1209-1224)
+    F->srows.resize(P->vals.size() + 1, -1);
+    F->scols.resize(P->vals.size() + 1, -1);
+    for (size_t id = 0; id < P->vals.size(); id++)
+      if (P->vals[id].weight) { F->srows[id] = P->vals[id].rows; F->scols[id] = P->vals[id].cols; }
+    {
+      int64_t in_w = 1;
+      for (auto& I : F->ins) {
+        if (I.op == Op::Matmul) { in_w = F->srows[I.in[1]]; break; }
+        if (I.op == Op::Embedding) break;
+      }
+      F->scols[F->x] = in_w;
+    }
+    // GEMM shapes from the B operand's static shape (a weight or a typed value)
+    for (auto& I : F->ins) {
+      if (I.op != Op::Matmul) continue;
+      I.k = F->srows[I.in[1]];
+      I.n = F->scols[I.in[1]];
+      if (I.k <= 0 || I.n <= 0) {
+        *err = "matmul operand '" + P->vals[I.in[1]].name + "' has no static shape";
+        return false;
+      }
+    }
+    // The reference's fusion pass (fusion.cpp:52-175): a GEMM whose result has
+    // one use absorbs the run of fusible ops that each consume the previous
+    // one's result and are used at most once (the last one any number of times
+    // when it ends the run... it must be used <= 1 unless it is last).
+    {
+      std::vector<int> uses(P->vals.size() + 1, 0);
+      for (auto& I : F->ins)
+        for (int v : I.in) uses[v]++;
+      for (size_t i = 0; i < F->ins.size(); i++) {
+        const Instr& lead = F->ins[i];
+        if (lead.op != Op::Matmul || uses[lead.res] != 1) continue;
+        size_t end = i + 1;
+        int consumed = lead.res;
+        while (end < F->ins.size()) {
+          const Instr& c = F->ins[end];
+          if (!is_fusible(c.op) || c.in.empty() || c.in[0] != consumed) break;
+          const bool last = end + 1 >= F->ins.size() || !is_fusible(F->ins[end + 1].op) ||
+                            F->ins[end + 1].in.empty() || F->ins[end + 1].in[0] != c.res;
+          if (uses[c.res] > 1 || (!last && uses[c.res] == 0)) break;
+          consumed = c.res;
+          end++;
+        }
+        if (end == i + 1) continue;
+        if (F->train) {
+          *err = "fused epilogue groups in train() are not supported (the reference's train core skips them)";
+          return false;
+        }
+        for (size_t j = i + 1; j < end; j++) {
+          F->ins[j].in_group = true;
+          F->ins[j].group_n = lead.n;
+        }
+        i = end - 1;
+      }
+    }
+    if (F->train) {
+      for (auto& I : F->ins)
+        if (I.op == Op::Binop || I.op == Op::Constant || (I.op >= Op::Transpose && I.op <= Op::Scatter)) {
+          *err = "binop / data-movement instructions in train() are not supported (the reference's train core "
+                 "skips them)";
+          return false;
+        }
+    }
     // column widths: static result types first, then the reference's
     // forward propagation (codegen.cpp:2721-2741).
     F->width.assign(P->vals.size() + 1, -1);
@@ -321,7 +461,8 @@ Plan* parse_plan(const char* text, std::string* err) {
     }
     for (auto& I : F->ins) {
       if (I.res < 0) continue;
-      if (I.op == Op::Matmul) F->width[I.res] = P->vals[I.in[1]].cols;
+      if (I.op == Op::Matmul) F->width[I.res] = I.n;
+      else if (I.op == Op::Constant) F->width[I.res] = 1;
       else if (!I.in.empty() && F->width[I.res] <= 0 && F->width[I.in[0]] > 0)
         F->width[I.res] = F->width[I.in[0]];
     }
@@ -346,12 +487,16 @@ Plan* parse_plan(const char* text, std::string* err) {
     for (auto& I : F.ins)
       if (I.res >= 0 && I.res == F.ret) out_c = rtcols(I.res);
     for (auto& I : F.ins) {
+      if (I.in_group) continue;  // absorbed by a GEMM group: not in the emitted list
       if (I.op == Op::Matmul) {
-        if (in_c < 0) in_c = P->vals[I.in[1]].rows;
-        out_c = P->vals[I.in[1]].cols;
+        if (in_c < 0) in_c = I.k;
+        out_c = I.n;
       }
       if (I.op == Op::Embedding && in_c < 0) in_c = 1;
-      if ((I.op == Op::Attention || I.op == Op::LayerNorm || I.op == Op::Moe) && I.res >= 0) {
+      if ((I.op == Op::Attention || I.op == Op::LayerNorm || I.op == Op::Moe || I.op == Op::Softmax ||
+           I.op == Op::Concat || I.op == Op::Slice || I.op == Op::Index || I.op == Op::Scatter ||
+           I.op == Op::Transpose || I.op == Op::Reshape) &&
+          I.res >= 0) {
         const int64_t c = rtcols(I.res);
         if (c > 0) out_c = c;
       }

@@ -1,6 +1,8 @@
 // Network plan: the instruction list of `nsc --mlir` (printer at
 // /root/reference/src/mlir/mlir_compiler.cpp:949-1025), resolved into value
-// ids, weight offsets and per-op attributes.  Pure host code.
+// ids, weight offsets and per-op attributes.  Attributes that printer drops
+// arrive as key=value tokens in the instruction comment (initial=, op=,
+// value=, axis=, start=, stop=, idx=).  Pure host code.
 #pragma once
 #include <cstdint>
 #include <map>
@@ -15,7 +17,9 @@ enum class Op {
   Alloc, Marker, Matmul, Act, Dropout, LayerNorm, Embedding, Attention, Moe, CrossEntropy,
   LossGrad, MatmulGradA, MatmulGradW, ActGrad, LayerNormGrad, EmbeddingGradW,
   AttnGradX, AttnGradWq, AttnGradWk, AttnGradWv, AttnGradWo,
-  MoeGradX, MoeGradWg, MoeGradWe1, MoeGradWe2, OptStep
+  MoeGradX, MoeGradWg, MoeGradWe1, MoeGradWe2, OptStep,
+  // forward-only ops (codegen.cpp:2007-2018, 2027-2033, 2079-2203)
+  Binop, Softmax, Constant, Transpose, Concat, Reshape, Slice, Index, Scatter
 };
 
 struct Instr {
@@ -26,6 +30,17 @@ struct Instr {
   int64_t rt_cols = -1;       // column count from the printed result type
   int heads = 1;              // Attention / AttnGrad*
   bool fused_away = false;    // Act folded into the preceding Matmul
+  // Epilogue absorbed into a GEMM group by the reference's fusion pass
+  // (fusion.cpp:52-175): binops become the identity, softmax / layernorm
+  // run over rows of the GEMM's N (codegen.cpp:2052-2076).
+  bool in_group = false;
+  int64_t group_n = 0;
+  int64_t k = 0, n = 0;       // Matmul: static K, N of the B operand
+  int binop = 0;              // Binop: 0 +, 1 -, 2 *, 3 /
+  int axis = 1;               // Concat / Slice / Index / Scatter
+  int64_t start = 0, stop = 0;  // Slice
+  std::vector<int64_t> idx;   // Index / Scatter
+  float value = 0.f;          // Constant
 };
 
 struct Value {
@@ -43,6 +58,9 @@ struct Func {
   int x = -1;  // runtime data input
   int y = -1;  // labels (training)
   std::vector<int64_t> width;  // propagated column count per value id (-1 unknown)
+  // the emitted code's static shape table (codegen.cpp:1170-1224):
+  // per value id, rows / cols from result types and weight shapes, -1 = dynamic
+  std::vector<int64_t> srows, scols;
 };
 
 struct MoeInfo {

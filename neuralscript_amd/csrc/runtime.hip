@@ -73,6 +73,7 @@ struct ns_model {
   std::vector<size_t> last_numel;
   std::vector<Buf> arena;         // per value id
   std::map<std::string, Buf> scratch;
+  std::map<int, int64_t*> dev_idx;  // Index / Scatter index lists on the device, by result id
   // profiling
   bool prof = false;
   std::vector<ProfEntry> pending;
@@ -248,9 +249,12 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
   hipStream_t s = m->stream;
   switch (I.op) {
     case Op::Matmul: {
-      const Value& B = P.vals[I.in[1]];
-      const int64_t K = B.rows, N = B.cols;
+      const int64_t K = I.k, N = I.n;  // B: a weight or a statically shaped value
       const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)K);
+      if (fr.numel[I.in[1]] < (size_t)(K * N)) {
+        set_error("matmul: operand '" + P.vals[I.in[1]].name + "' is smaller than its static shape");
+        return -1;
+      }
       NSH_OUT(C, I.res, (size_t)(M * N));
       Prof p(m, I.act ? "gemm_act" : "gemm");
       return rt_gemm(m, fr.ptr[I.in[0]], fr.ptr[I.in[1]], C, M, N, K, K, N, N, false, false, I.act);
@@ -277,6 +281,7 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       // row width: the result type's columns, else the input's
       // (codegen.cpp:2021 forward, :2744-2751 train)
       int64_t last = train ? F.width[I.in[0]] : (I.rt_cols > 0 ? I.rt_cols : F.width[I.in[0]]);
+      if (I.in_group) last = I.group_n;  // inside a GEMM group: rows of N (codegen.cpp:2066-2067)
       if (last <= 0) last = 1;
       const size_t n = fr.numel[I.in[0]];
       NSH_OUT(y, I.res, n);
@@ -344,6 +349,129 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       m->moe_last_m = M;
       Prof p(m, "moe_experts");  // the two grouped expert GEMMs
       return launch_moe_experts(fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]], w, out, M, q.D, q.H, q.E, s);
+    }
+    case Op::Binop: {
+      const size_t na = fr.numel[I.in[0]];
+      if (I.in_group) {  // operator-less binop inside a GEMM group: identity (codegen.cpp:2073-2075)
+        fr.numel[I.res] = na;
+        fr.ptr[I.res] = fr.ptr[I.in[0]];
+        return 0;
+      }
+      // the raw input as right operand reads the emitted code's never-filled
+      // buf_x (codegen.cpp:2014-2016): an empty B, i.e. B = 0
+      const size_t nb = I.in[1] == F.x ? 0 : fr.numel[I.in[1]];
+      NSH_OUT(c, I.res, na);
+      Prof p(m, "binop");
+      return launch_binop(fr.ptr[I.in[0]], fr.ptr[I.in[1]], c, (int64_t)na, (int64_t)nb, I.binop, s);
+    }
+    case Op::Softmax: {
+      // rows of: the group's N; train: the input's width (codegen.cpp:2860-2873);
+      // else the result's, the input's static columns, or 1 (codegen.cpp:2027-2033)
+      int64_t last;
+      if (I.in_group) last = I.group_n;
+      else if (train) last = F.width[I.in[0]];
+      else last = F.scols[I.res] > 0 ? F.scols[I.res] : F.scols[I.in[0]];
+      if (last <= 0) last = 1;
+      const size_t n = fr.numel[I.in[0]];
+      NSH_OUT(y, I.res, n);
+      Prof p(m, "softmax");
+      return launch_softmax(fr.ptr[I.in[0]], y, (int64_t)n, last, s);
+    }
+    case Op::Constant: {
+      NSH_OUT(y, I.res, 1);
+      return launch_fill(y, 1, I.value, s);
+    }
+    case Op::Reshape:  // a copy of the input's values (codegen.cpp:2124-2128)
+      fr.numel[I.res] = fr.numel[I.in[0]];
+      fr.ptr[I.res] = fr.ptr[I.in[0]];
+      return 0;
+    case Op::Transpose: {
+      const int64_t C = F.scols[I.in[0]] > 0 ? F.scols[I.in[0]] : 1;
+      const size_t n = fr.numel[I.in[0]];
+      const int64_t R = F.srows[I.in[0]] > 0 ? F.srows[I.in[0]] : (int64_t)(n / (size_t)C);
+      if ((size_t)(R * C) > n) {
+        set_error("transpose: static shape exceeds the operand");
+        return -1;
+      }
+      NSH_OUT(y, I.res, (size_t)(R * C));
+      Prof p(m, "movement");
+      return launch_transpose(fr.ptr[I.in[0]], y, R, C, s);
+    }
+    case Op::Concat: {
+      const size_t na = fr.numel[I.in[0]], nb = fr.numel[I.in[1]];
+      Prof p(m, "movement");
+      if (I.axis == 0) {  // ns_concat0: rows of a, then rows of b
+        const int64_t D = F.scols[I.in[0]] > 0 ? F.scols[I.in[0]] : 1;
+        const int64_t ba = (int64_t)(na / (size_t)D), bb = (int64_t)(nb / (size_t)D);
+        NSH_OUT(y, I.res, (size_t)((ba + bb) * D));
+        if (launch_copy(fr.ptr[I.in[0]], y, ba * D, s) != 0) return -1;
+        return launch_copy(fr.ptr[I.in[1]], y + ba * D, bb * D, s);
+      }
+      const int64_t ca = F.scols[I.in[0]] > 0 ? F.scols[I.in[0]] : 1;
+      const int64_t cb = F.scols[I.in[1]] > 0 ? F.scols[I.in[1]] : 1;
+      const int64_t R = (int64_t)(na / (size_t)ca);
+      if ((size_t)(R * cb) > nb) {
+        set_error("concat: the second operand has fewer rows than the first");
+        return -1;
+      }
+      NSH_OUT(y, I.res, (size_t)(R * (ca + cb)));
+      return launch_concat_cols(fr.ptr[I.in[0]], fr.ptr[I.in[1]], y, R, ca, cb, s);
+    }
+    case Op::Slice: {
+      const int64_t C = F.scols[I.in[0]] > 0 ? F.scols[I.in[0]] : 1;
+      const size_t n = fr.numel[I.in[0]];
+      Prof p(m, "movement");
+      if (I.axis == 0) {  // rows [start, stop)
+        if ((size_t)(I.stop * C) > n) {
+          set_error("slice: row range beyond the operand");
+          return -1;
+        }
+        NSH_OUT(y, I.res, (size_t)((I.stop - I.start) * C));
+        return launch_copy(fr.ptr[I.in[0]] + I.start * C, y, (I.stop - I.start) * C, s);
+      }
+      if (I.stop > C) {
+        set_error("slice: column range beyond the row width");
+        return -1;
+      }
+      const int64_t M = (int64_t)(n / (size_t)C);
+      NSH_OUT(y, I.res, (size_t)(M * (I.stop - I.start)));
+      return launch_slice_cols(fr.ptr[I.in[0]], y, M, C, I.start, I.stop - I.start, s);
+    }
+    case Op::Index: case Op::Scatter: {
+      const int64_t C = F.scols[I.in[0]] > 0 ? F.scols[I.in[0]] : 1;
+      const size_t n = fr.numel[I.in[0]];
+      const int64_t L = (int64_t)I.idx.size();
+      const int64_t M = (int64_t)(n / (size_t)C);
+      // rows addressed: axis 1 -> columns of each row, axis 0 -> rows
+      // (scatter along rows: the operand's static rows, codegen.cpp:2188-2193)
+      const int64_t R = I.op == Op::Scatter && I.axis == 0 ? (F.srows[I.in[0]] > 0 ? F.srows[I.in[0]] : 0) : M;
+      const int64_t bound = I.axis == 1 ? C : (I.op == Op::Index ? M : R);
+      for (int64_t v : I.idx)
+        if (v < 0 || v >= bound) {
+          set_error(std::string(I.op == Op::Index ? "index" : "scatter") + ": index " + std::to_string(v) +
+                    " out of range");
+          return -1;
+        }
+      if (I.op == Op::Scatter) {
+        const size_t need = I.axis == 1 ? (size_t)(M * L) : (size_t)(L * C);
+        if ((size_t)(R * C) > n || fr.numel[I.in[1]] < need) {
+          set_error("scatter: operand or update smaller than its static shape");
+          return -1;
+        }
+      }
+      int64_t*& d = m->dev_idx[I.res];
+      if (!d && L > 0) {
+        NSH_CHECK(hipMalloc(&d, (size_t)L * sizeof(int64_t)));
+        NSH_CHECK(hipMemcpy(d, I.idx.data(), (size_t)L * sizeof(int64_t), hipMemcpyHostToDevice));
+      }
+      Prof p(m, "movement");
+      if (I.op == Op::Index) {
+        NSH_OUT(y, I.res, (size_t)(I.axis == 1 ? M * L : L * C));
+        return launch_index(fr.ptr[I.in[0]], d, y, M, C, L, I.axis == 1 ? 1 : 0, s);
+      }
+      NSH_OUT(y, I.res, (size_t)(I.axis == 1 ? M * C : R * C));
+      return launch_scatter(fr.ptr[I.in[0]], d, fr.ptr[I.in[1]], y, I.axis == 1 ? M : R, C, L, I.axis == 1 ? 1 : 0,
+                            s);
     }
     case Op::Dropout:
       if (train) {
@@ -554,7 +682,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
     if (skip[ii] || I.op == Op::Marker) continue;
     switch (I.op) {
       case Op::Matmul: case Op::Act: case Op::Embedding: case Op::LayerNorm: case Op::Attention: case Op::Moe:
-      case Op::Dropout:
+      case Op::Dropout: case Op::Softmax:
         if (exec_forward_op(m, F, I, fr, true) != 0) return -1;
         break;
       case Op::CrossEntropy: {
@@ -867,6 +995,7 @@ void nsh_model_free(ns_model* m) {
   if (m->stream) hipStreamSynchronize(m->stream);
   for (auto& b : m->arena) if (b.p) hipFree(b.p);
   for (auto& kv : m->scratch) if (kv.second.p) hipFree(kv.second.p);
+  for (auto& kv : m->dev_idx) if (kv.second) hipFree(kv.second);
   for (auto& e : m->pending) { hipEventDestroy(e.a); hipEventDestroy(e.b); }
   for (auto e : m->event_pool) hipEventDestroy(e);
   if (m->d_w) hipFree(m->d_w);

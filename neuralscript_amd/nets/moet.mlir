@@ -6,7 +6,7 @@ ns.func @MoET {
   ns.tensor.alloc %moe_e2_w : Tensor[8, 1536] float32 // allocate MoE expert FFN-2 [8, 48 -> 32]
   ns.tensor.alloc %fc_w : Tensor[32, 16] float32 // allocate weight [32, 16]
   ns.layer.embedding %emb0 %emb_w %x : Tensor[Dynamic, 32] float32 // embedding(x, emb_w)
-  ns.layer.moe %moe1 %emb0 %moe_g_w %moe_e1_w %moe_e2_w : Tensor[Dynamic, 32] float32 // moe(emb0, experts=8, initial=6, ffn=48)
+  ns.layer.moe %moe1 %emb0 %moe_g_w %moe_e1_w %moe_e2_w : Tensor[Dynamic, 32] float32 // moe(emb0, experts=8, ffn=48) initial=6
   ns.matmul %fc2 %moe1 %fc_w // moe1 -> fc
   ns.return %fc2
 }
@@ -18,7 +18,7 @@ ns.func @MoET_train {
   ns.tensor.alloc %fc_w : Tensor[32, 16] float32 // allocate weight [32, 16]
   ns.grad // gradient block (forward)
   ns.layer.embedding %emb3 %emb_w %x : Tensor[Dynamic, 32] float32 // embedding(x, emb_w)
-  ns.layer.moe %moe4 %emb3 %moe_g_w %moe_e1_w %moe_e2_w : Tensor[Dynamic, 32] float32 // moe(emb3, experts=8, initial=6, ffn=48)
+  ns.layer.moe %moe4 %emb3 %moe_g_w %moe_e1_w %moe_e2_w : Tensor[Dynamic, 32] float32 // moe(emb3, experts=8, ffn=48) initial=6
   ns.matmul %mm5 %moe4 %fc_w : Tensor[B, 16] float32 // moe4 @ fc_w
   ns.cross_entropy %f6 %mm5 %labels // cross_entropy()
   ns.grad.loss %g7 %mm5 %labels // d(cross_entropy)/d(preds)

@@ -1,12 +1,12 @@
 """Regenerate neuralscript_amd/nets/<net>.mlir from oracle/nets/<net>.ns with
-the reference compiler built by oracle/Makefile (oracle/_ref/nsc --mlir).
-
-The printer drops MoE(initial_experts: K0); it is restored as `initial=K0`
-in the ns.layer.moe comment, the key libnship's plan parser reads.
+oracle/_ref/irdump, built by oracle/Makefile against the reference compiler's
+own objects: the text of `nsc --mlir`, plus the instruction attributes that
+printer drops (MoE initial experts, binop operator, slice/index/scatter/concat
+arguments, constants) as key=value tokens at the end of each comment -- the
+keys libnship's plan parser reads.
 Runs in the build container only (it needs the reference build).
 """
 import os
-import re
 import subprocess
 import sys
 
@@ -15,12 +15,7 @@ OUT = os.path.join(os.path.dirname(HERE), "neuralscript_amd", "nets")
 
 
 def ir_of(ns_path):
-    text = subprocess.check_output([os.path.join(HERE, "_ref", "nsc"), ns_path, "--mlir"]).decode()
-    src = open(ns_path).read()
-    m = re.search(r"initial_experts:\s*(\d+)", src)
-    if m:
-        text = re.sub(r"(// moe\([^)]*?)(ffn=)", r"\g<1>initial=%s, \g<2>" % m.group(1), text)
-    return text
+    return subprocess.check_output([os.path.join(HERE, "_ref", "irdump"), ns_path]).decode()
 
 
 def main(names):

@@ -175,6 +175,23 @@ EXPORT void or_layernorm(const float* in, float* out, size_t numel, int64_t last
     }
 }
 
+/* ns_softmax codegen.cpp:1293-1303: out = copy of in, then every full row
+ * of `last` values: max (std::max order), expf(x - max) summed in order,
+ * then divided by the sum. */
+EXPORT void or_softmax(const float* in, float* out, size_t numel, int64_t last) {
+    if (out != in) memcpy(out, in, numel * sizeof(float));
+    const int64_t rows = (int64_t)numel / last;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < rows; r++) {
+        float* m = out + (size_t)r * last;
+        float mx = m[0];
+        for (int64_t j = 1; j < last; j++) mx = (mx < m[j]) ? m[j] : mx;
+        float s = 0.f;
+        for (int64_t j = 0; j < last; j++) { m[j] = expf(m[j] - mx); s += m[j]; }
+        for (int64_t j = 0; j < last; j++) m[j] /= s;
+    }
+}
+
 /* ns_layernorm_grad codegen.cpp:1346-1371 */
 EXPORT void or_layernorm_grad(const float* dout, const float* x, float* dx,
                               size_t numel, int64_t last) {

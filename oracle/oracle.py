@@ -64,6 +64,7 @@ def lib():
             "or_matmul_grad_a": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
             "or_matmul_grad_w": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
             "or_layernorm": (None, [_f32p, _f32p, sz, i64]),
+            "or_softmax": (None, [_f32p, _f32p, sz, i64]),
             "or_layernorm_grad": (None, [_f32p, _f32p, _f32p, sz, i64]),
             "or_embedding": (None, [_f32p, _f32p, _f32p, i64, i64, i64]),
             "or_embedding_rows": (None, [_f32p, _i64p, i64, i64]),
@@ -167,6 +168,12 @@ def layernorm(x, last):
     y = empty(x.size)
     lib().or_layernorm(fp(x), fp(y), x.size, last)
     return y
+
+
+def softmax(x, last):
+    out = empty(x.size)
+    lib().or_softmax(fp(x), fp(out), x.size, last)
+    return out
 
 
 def layernorm_grad(dout, x, last):
@@ -338,6 +345,58 @@ def comment_attr(comment, key):
     return int(m.group(1)) if m else None
 
 
+def comment_str(comment, key):
+    """Raw value of key=VALUE in an instruction comment (oracle/irdump), or None."""
+    m = re.search(r"(?:^|\s)%s=(\S*)" % re.escape(key), comment)
+    return m.group(1) if m else None
+
+
+# Ops the reference's fusion pass may append to a GEMM (fusion.cpp:23-40).
+_FUSIBLE = {"ns.activation." + k for k in ("relu", "leaky_relu", "sigmoid", "tanh", "swish", "gelu", "silu",
+                                           "identity", "softmax")} | {"ns.layernorm", "ns.subview_binop"}
+
+
+def fusion_groups(f):
+    """The reference fusion pass (fusion.cpp:52-94, 97-175) on one function:
+    {index of an absorbed epilogue instruction: N of its GEMM}.  Inside a
+    group the emitted code applies activations as usual, layernorm and
+    softmax over rows of N, and -- the binop's operator symbol being empty
+    (the lexer gives operator tokens no text) -- a binop as the identity
+    activation (codegen.cpp:2052-2076)."""
+    ins = f.instrs
+    uses = {}
+    for i in ins:
+        for o in i.operands:
+            uses[o] = uses.get(o, 0) + 1
+    out = {}
+    i = 0
+    while i < len(ins):
+        lead = ins[i]
+        if lead.op != "ns.matmul" or uses.get(lead.result, 0) != 1:
+            i += 1
+            continue
+        end, consumed = i + 1, lead.result
+        while end < len(ins):
+            c = ins[end]
+            if c.op not in _FUSIBLE or not c.operands or c.operands[0] != consumed:
+                break
+            nxt = ins[end + 1] if end + 1 < len(ins) else None
+            is_last = (nxt is None or nxt.op not in _FUSIBLE or not nxt.operands or
+                       nxt.operands[0] != c.result)
+            u = uses.get(c.result, 0)
+            if u > 1 or (not is_last and u == 0):
+                break
+            consumed = c.result
+            end += 1
+        if end > i + 1:
+            for j in range(i + 1, end):
+                out[j] = lead.operands[1]  # the GEMM's weight; N = its columns
+            i = end
+        else:
+            i += 1
+    return out
+
+
 class Net:
     """Static facts of a network: weights in TENSOR_ALLOC order, geometry."""
 
@@ -372,7 +431,41 @@ class Net:
                     if k0 <= 0 or k0 > E:
                         k0 = E
                     self.moe = dict(D=D, E=E, H=H, K0=k0, g=i.operands[1])
+        self.fused = {f.name: fusion_groups(f) for f in self.funcs}
         self.in_cols, self.out_cols = self._geometry()
+
+    def ids_table(self, f):
+        """The emitted code's static (rows, cols) per value id, -1 = dynamic
+        (codegen.cpp:1170-1224): result types, weight shapes, and the input's
+        width (first GEMM's K, 1 for embedding-first or anything else)."""
+        t = {}
+        for i in f.instrs:
+            if i.result and i.op != "ns.tensor.alloc":
+                d = i.dims or []
+                t[i.result] = (d[0] if len(d) > 0 else -1, d[1] if len(d) > 1 else -1)
+        for n, r, c in self.weights:
+            t[n] = (r, c)
+        in_w = 1
+        for i in f.instrs:
+            if i.op == "ns.matmul" and len(i.operands) >= 2:
+                in_w = self._static_dims(f, i.operands[1])[0]
+                break
+            if i.op == "ns.layer.embedding":
+                break
+        xid = _input_id(f, set(self.shape))
+        if xid is not None:  # codegen.cpp:1209-1224: the input's cols become in_w
+            t[xid] = (t.get(xid, (-1, -1))[0], in_w)
+        return t
+
+    def _static_dims(self, f, vid):
+        """(rows, cols) of a GEMM's B operand: a weight's shape, or the
+        static result type of the instruction that produced it."""
+        if vid in self.shape:
+            return self.shape[vid]
+        for i in f.instrs:
+            if i.result == vid and i.dims:
+                return (i.dims[0] if len(i.dims) > 0 else -1, i.dims[1] if len(i.dims) > 1 else -1)
+        return (-1, -1)
 
     def _rt_cols(self, f, vid):
         for i in f.instrs:
@@ -386,18 +479,24 @@ class Net:
         """in_cols / out_cols as the emitted driver computes them
         (codegen.cpp:2295-2320)."""
         f = self.fwd
+        absorbed = fusion_groups(f)
         in_cols = out_cols = -1
         for i in f.instrs:
             if i.op != "ns.tensor.alloc" and i.result and i.result == f.ret:
                 out_cols = self._rt_cols(f, i.result)
-        for i in f.instrs:
+        for k, i in enumerate(f.instrs):
+            if k in absorbed:
+                continue
             if i.op == "ns.matmul" and len(i.operands) >= 2:
+                r, c = self._static_dims(f, i.operands[1])
                 if in_cols < 0:
-                    in_cols = self.shape[i.operands[1]][0]
-                out_cols = self.shape[i.operands[1]][1]
+                    in_cols = r
+                out_cols = c
             if i.op == "ns.layer.embedding" and in_cols < 0:
                 in_cols = 1
-            if i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe") and i.result:
+            if (i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe", "ns.activation.softmax",
+                         "ns.concat", "ns.slice", "ns.index", "ns.scatter", "ns.transpose", "ns.reshape")
+                    and i.result):
                 c = self._rt_cols(f, i.result)
                 if c > 0:
                     out_cols = c
@@ -410,7 +509,10 @@ class Net:
 def _act_of(f, pre):
     for i in f.instrs:
         if i.op.startswith("ns.activation.") and i.operands and i.operands[0] == pre:
-            return ACT_CODES[i.op.split(".")[-1]]
+            kind = i.op.split(".")[-1]
+            # softmax's ACTIVATION_GRAD carries "softmax", derivative code 0 = 1
+            # (mlir_compiler.cpp:348-360, codegen.cpp:3074-3081, 1305-1315)
+            return 0 if kind == "softmax" else ACT_CODES[kind]
     raise ValueError(f"no activation consumes {pre}")
 
 
@@ -420,7 +522,8 @@ def _input_id(f, weights):
             return i.operands[1]
         if i.op == "ns.matmul" and i.operands and i.operands[0] not in weights:
             return i.operands[0]
-        if i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe", "ns.dropout") or \
+        if i.op in ("ns.layer.attention", "ns.layernorm", "ns.layer.moe", "ns.dropout", "ns.transpose",
+                    "ns.concat", "ns.reshape", "ns.slice", "ns.index", "ns.scatter") or \
                 i.op.startswith("ns.activation."):
             if i.operands and i.operands[0] not in weights:
                 return i.operands[0]
@@ -481,13 +584,129 @@ class Model:
 
         grads = {}
         loss = None
-        for i in f.instrs:
+        fused = net.fused[f.name]
+        if fused and f.is_train:
+            raise NotImplementedError("fused epilogue groups in a train function")
+        ids = net.ids_table(f)
+
+        def idr(v):
+            return ids.get(v, (-1, -1))[0]
+
+        def idc(v):
+            return ids.get(v, (-1, -1))[1]
+
+        for k, i in enumerate(f.instrs):
             op, o = i.op, i.operands
             if op in ("ns.tensor.alloc", "ns.grad", "ns.forward"):
                 continue
+            if k in fused and op in ("ns.subview_binop", "ns.layernorm", "ns.activation.softmax"):
+                N = net.shape[fused[k]][1]
+                src = val(o[0])
+                if op == "ns.subview_binop":  # operator-less binop = identity activation
+                    buf[i.result] = src.copy()
+                elif op == "ns.layernorm":
+                    buf[i.result] = layernorm(src, N)
+                else:
+                    buf[i.result] = softmax(src, N)
+                width[i.result] = N
+                continue
+            if op in ("ns.subview_binop", "ns.constant", "ns.transpose", "ns.concat", "ns.reshape", "ns.slice",
+                      "ns.index", "ns.scatter") and f.is_train:
+                raise NotImplementedError(op + " in a train function (the reference's train core skips it)")
+            if op == "ns.activation.softmax":
+                src = val(o[0])
+                if f.is_train:  # train core: rows of the input's width (codegen.cpp:2860-2873)
+                    last = cols(o[0]) if cols(o[0]) > 0 else 1
+                else:  # codegen.cpp:2027-2033
+                    last = idc(i.result) if idc(i.result) > 0 else (idc(o[0]) if idc(o[0]) > 0 else 1)
+                buf[i.result] = softmax(src, last)
+                width[i.result] = last
+                continue
+            if op == "ns.subview_binop":  # ns_binop, codegen.cpp:1267-1278 / 2007-2018
+                a = val(o[0])
+                b = np.zeros(0, np.float32) if o[1] == xid else val(o[1])
+                code = {"-": 1, "*": 2, "/": 3}.get(comment_str(i.comment, "op") or "", 0)
+                bb = np.resize(b, a.size) if b.size else np.zeros(a.size, np.float32)
+                with np.errstate(all="ignore"):
+                    buf[i.result] = [a + bb, a - bb, a * bb, a / bb][code].astype(np.float32)
+                width[i.result] = cols(o[0])
+                continue
+            if op == "ns.constant":
+                v = comment_str(i.comment, "value")
+                if v is None:
+                    v = i.comment.split()[-1]
+                buf[i.result] = np.array([np.float32(float(v))], np.float32)
+                continue
+            if op == "ns.reshape":
+                buf[i.result] = val(o[0]).copy()
+                width[i.result] = idc(i.result)
+                continue
+            if op == "ns.transpose":  # ns_transpose2d, codegen.cpp:1638-1644 / 2082-2100
+                a = val(o[0])
+                C = idc(o[0]) if idc(o[0]) > 0 else 1
+                R = idr(o[0]) if idr(o[0]) > 0 else a.size // C
+                buf[i.result] = np.ascontiguousarray(a[:R * C].reshape(R, C).T).ravel()
+                width[i.result] = R
+                continue
+            if op == "ns.concat":  # ns_concat2 / ns_concat0, codegen.cpp:1646-1661 / 2102-2123
+                a, b = val(o[0]), val(o[1])
+                if comment_str(i.comment, "axis") == "0":
+                    D = idc(o[0]) if idc(o[0]) > 0 else 1
+                    Ba, Bb = a.size // D, b.size // D
+                    buf[i.result] = np.concatenate([a[:Ba * D], b[:Bb * D]])
+                else:
+                    Ca = idc(o[0]) if idc(o[0]) > 0 else 1
+                    Cb = idc(o[1]) if idc(o[1]) > 0 else 1
+                    R = a.size // Ca
+                    buf[i.result] = np.concatenate([a[:R * Ca].reshape(R, Ca), b[:R * Cb].reshape(R, Cb)],
+                                                   axis=1).ravel()
+                    width[i.result] = Ca + Cb
+                continue
+            if op == "ns.slice":  # ns_slice2 / ns_slicerows, codegen.cpp:1663-1676 / 2129-2150
+                a = val(o[0])
+                ax, s0, e0 = (int(comment_str(i.comment, kk)) for kk in ("axis", "start", "stop"))
+                C = idc(o[0]) if idc(o[0]) > 0 else 1
+                if ax == 0:
+                    buf[i.result] = a[s0 * C:e0 * C].copy()
+                else:
+                    M = a.size // C
+                    buf[i.result] = np.ascontiguousarray(a[:M * C].reshape(M, C)[:, s0:e0]).ravel()
+                    width[i.result] = e0 - s0
+                continue
+            if op in ("ns.index", "ns.scatter"):  # codegen.cpp:1678-1709 / 2151-2203
+                a = val(o[0])
+                ax = int(comment_str(i.comment, "axis"))
+                idx = [int(t) for t in (comment_str(i.comment, "idx") or "").split(",") if t]
+                C = idc(o[0]) if idc(o[0]) > 0 else 1
+                L = len(idx)
+                if op == "ns.index":
+                    if ax == 0:
+                        buf[i.result] = np.concatenate([a[j * C:(j + 1) * C] for j in idx]) if L else empty(0)
+                    else:
+                        M = a.size // C
+                        buf[i.result] = np.ascontiguousarray(a[:M * C].reshape(M, C)[:, idx]).ravel()
+                        width[i.result] = L
+                else:
+                    u = val(o[1])
+                    if ax == 0:
+                        R = idr(o[0]) if idr(o[0]) > 0 else 0
+                        out = a[:R * C].copy()
+                        for kk, j in enumerate(idx):
+                            out[j * C:(j + 1) * C] = u[kk * C:(kk + 1) * C]
+                    else:
+                        M = a.size // C
+                        out = a[:M * C].copy().reshape(M, C)
+                        for kk, j in enumerate(idx):
+                            out[:, j] = u[kk::L][:M] if L else out[:, j]
+                        out = out.ravel()
+                    buf[i.result] = out
+                    width[i.result] = C
+                continue
             if op == "ns.matmul":
                 A = val(o[0])
-                K, N = net.shape[o[1]]
+                K, N = net._static_dims(f, o[1])
+                if K <= 0 or N <= 0:
+                    raise ValueError(f"matmul {i.result}: operand {o[1]} has no static shape")
                 M = A.size // K
                 buf[i.result] = matmul(A, val(o[1]), M, K, N)
                 width[i.result] = N

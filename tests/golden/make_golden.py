@@ -25,7 +25,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "oracle"), os.path.join(ROOT, "tests")]
 
 import helpers  # noqa: E402
 import oracle  # noqa: E402
-from neuralscript_amd.abi import NsLib  # noqa: E402
+from neuralscript_amd.abi import NsLib, _fp  # noqa: E402
 
 XOR_X = np.array([0, 0, 0, 1, 1, 0, 1, 1], dtype=np.float32)
 XOR_Y = np.array([1, 0, 0, 1, 0, 1, 1, 0], dtype=np.float32)
@@ -43,6 +43,11 @@ CASES = [
     ("moet", 41, 109, 3, 0.01, False),
     ("c5s", 64, 110, 2, 0.003, False),
     ("moeb", 300, 111, 3, 0.01, False),
+    ("dmv", 37, 112, 0, 0.0, False),
+    ("dmw", 29, 113, 0, 0.0, False),
+    ("bop", 41, 114, 0, 0.0, False),
+    ("dmx", 23, 115, 0, 0.0, False),
+    ("smt", 33, 116, 3, 0.05, False),
 ]
 
 
@@ -65,6 +70,20 @@ def curve_lrs(base, steps=100):
     return [np.float32(base) * np.float32(oracle.lr_scale_cosine(t)) for t in range(steps)]
 
 
+def written(lib, m, x):
+    """ns_eval_infer's output, cut to the prefix the driver wrote: it copies
+    its result buffer, which for some data-movement programs is shorter than
+    ns_model_output_numel (two runs over differently pre-filled outputs)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    outs = []
+    for fill in (np.float32(-7.5e37), np.float32(3.25e37)):
+        o = np.full(lib.output_numel(m, x.size), fill, dtype=np.float32)
+        assert lib.lib.ns_eval_infer(m, _fp(x), _fp(o), x.size) == 0
+        outs.append(o)
+    diff = np.nonzero(outs[0].view(np.uint32) != outs[1].view(np.uint32))[0]
+    return outs[0][: diff[0]] if diff.size else outs[0]
+
+
 def digest(a):
     return hashlib.sha256(np.ascontiguousarray(a, dtype=np.float32).tobytes()).hexdigest()[:16]
 
@@ -77,7 +96,7 @@ def main(names=()):
         w = helpers.net_weights(name, seed)
         lib = NsLib(os.path.join(helpers.REF, f"lib{name}.so"))
         m = lib.init(w)
-        out = lib.eval_infer(m, x)[: net.output_numel(x.size) if net.moe is None else rows * net.moe["D"]]
+        out = written(lib, m, x)[: net.output_numel(x.size) if net.moe is None else rows * net.moe["D"]]
         rec = dict(out=out, x_digest=np.array(digest(x)), w_digest=np.array(digest(w)))
         if steps:
             rec["losses"] = np.array([lib.train_step(m, x, y, lr) for _ in range(steps)], dtype=np.float32)

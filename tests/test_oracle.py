@@ -45,7 +45,8 @@ def test_oracle_matches_reference_fixtures(case):
 @pytest.mark.skipif(not os.path.exists(os.path.join(helpers.REF, "libc5t.so")),
                     reason="reference build (oracle/_ref) not present")
 @pytest.mark.parametrize("name,rows", [("c2s", 41), ("c3s", 70), ("c4k", 64), ("c5t", 50), ("moet", 23), ("mlpt", 9),
-                                       ("moeb", 37)])
+                                       ("moeb", 37), ("dmv", 23), ("dmw", 31), ("bop", 19),
+                                       ("dmx", 17)])
 def test_oracle_matches_reference_build(name, rows):
     from neuralscript_amd.abi import NsLib
     net = oracle.Net(helpers.ir_text(name))
