@@ -85,7 +85,7 @@ namespace nship {
 namespace {
 
 int ensure(Buf& b, size_t n) {
-  if (n <= b.cap) return 0;
+  if (n <= b.cap && b.p) return 0;  // (an empty request still gets a buffer)
   if (b.p) NSH_CHECK(hipFree(b.p));
   b.p = nullptr;
   b.cap = 0;

@@ -40,6 +40,33 @@ def test_forward_matches_reference_fixture(case):
     lib.free(m)
 
 
+@pytest.mark.parametrize("name", FWD_NETS)
+def test_forward_of_an_empty_batch(name):
+    """ns_eval_infer with zero input rows returns 0 and writes nothing (the
+    reference's loops simply do not run); the model stays usable.  dmx slices
+    rows 1..2 of a batch-sized value, which the reference would read out of
+    bounds: there the call returns -1 instead."""
+    print(f"empty batch {name}", flush=True)
+    case = next(c for c in CASES if c[0] == name)
+    net, x, _ = case_inputs(name, case[1], case[2])
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, case[2]))
+    assert lib.output_numel(m, 0) == 0
+    empty = np.zeros(0, np.float32)
+    if name == "dmx":
+        with pytest.raises(RuntimeError):
+            lib.eval_infer(m, empty)
+    else:
+        assert lib.eval_infer(m, empty).size == 0
+    out = lib.eval_infer(m, x)
+    g = golden(name)["out"]
+    if name in BITWISE:
+        assert helpers.bitwise_equal(out[: g.size], g)
+    else:
+        helpers.assert_close(out[: g.size], g, f"{name} forward after an empty batch")
+    lib.free(m)
+
+
 def test_c2_full_size_rows_match_oracle():
     """Config 2 at its full batch (8192 x 1024 -> 4096 -> 4096 -> 1024, GELU);
     the oracle recomputes 96 rows spread over the batch (rows are independent)."""
