@@ -127,12 +127,17 @@ __device__ __forceinline__ void read_frag(const float* __restrict__ lds, int row
   }
 }
 
-// Logical tile of workgroup b: XCD-contiguous runs, then 8-row groups.
-__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int T = tiles_m * tiles_n;
+// Workgroup b of T -> a linear index such that each XCD (ids are dealt
+// round-robin over the 8 XCDs) owns one contiguous run; a bijection on [0, T).
+__device__ __forceinline__ int xcd_linear(int b, int T) {
   const int per = T >> 3, rem = T & 7;
   const int x = b & 7, i = b >> 3;
-  const int L = x * per + (x < rem ? x : rem) + i;
+  return x * per + (x < rem ? x : rem) + i;
+}
+
+// Logical tile of workgroup b: XCD-contiguous runs, then 8-row groups.
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int L = xcd_linear(b, tiles_m * tiles_n);
   const int group = 8 * tiles_n;
   const int first_m = (L / group) * 8;
   const int gsize = min(tiles_m - first_m, 8);
@@ -176,13 +181,16 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
   int m0, n0;
   if (g.groups) {
     // Grouped: tile entry -> (group, m tile); rows [seg[e], seg[e+1]) of the
-    // group, B advanced by e * sBg.  Surplus workgroups exit (uniformly).
-    const int entry = blockIdx.x / tiles_n;
+    // group, B advanced by e * sBg.  Entries run XCD-contiguously with all
+    // their n tiles, so a gathered A tile is fetched into one XCD's L2 only.
+    // Surplus workgroups exit (uniformly).
+    const int L = xcd_linear(blockIdx.x, gridDim.x);
+    const int entry = L / tiles_n;
     if (entry >= *g.ntiles) return;
     const int e = g.tiles[2 * entry], mt = g.tiles[2 * entry + 1];
     m0 = g.seg[e] + mt * BM;
     m_end = g.seg[e + 1];
-    n0 = (blockIdx.x % tiles_n) * BN;
+    n0 = (L % tiles_n) * BN;
     B += (int64_t)e * g.sBg;
   } else {
     int tm, tn;
