@@ -148,7 +148,8 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
-template <bool TA, bool TB, bool VEC>
+// PLAIN: no row gather/scatter, no row scale, epilogue mode kEpiAct.
+template <bool TA, bool TB, bool VEC, bool PLAIN>
 __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
   const int M = g.M, N = g.N, K = g.K;
   const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
@@ -251,6 +252,35 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
 
   // Accumulator v of lane (l32, kh) in a 32x32 block sits at
   // row 8*(v/4) + 4*kh + v%4, column l32.
+  if constexpr (PLAIN) {
+    // plain stores, the activation resolved once per 32x32 block
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int col = n0 + wn * 64 + c * 32 + l32;
+        const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
+        float* __restrict__ cp = C + (int64_t)row0 * ldc + col;
+        const bool cin = col < N;
+#define NSH_STORE16(CODE)                                                          \
+  _Pragma("unroll") for (int v = 0; v < 16; v++) {                                 \
+    const int dr = 8 * (v >> 2) + (v & 3);                                         \
+    if (cin && row0 + dr < m_end) cp[(int64_t)dr * ldc] = act_apply(acc[r][c][v], CODE); \
+  }
+        switch (g.act) {
+          case kActRelu: NSH_STORE16(kActRelu); break;
+          case kActLeaky: NSH_STORE16(kActLeaky); break;
+          case kActSigmoid: NSH_STORE16(kActSigmoid); break;
+          case kActTanh: NSH_STORE16(kActTanh); break;
+          case kActSilu: NSH_STORE16(kActSilu); break;
+          case kActGelu: NSH_STORE16(kActGelu); break;
+          case kActGeluMoe: NSH_STORE16(kActGeluMoe); break;
+          default: NSH_STORE16(kActId); break;
+        }
+#undef NSH_STORE16
+      }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 2; r++)
 #pragma unroll
@@ -291,7 +321,12 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   const int entries = g.groups ? g.tiles_m + g.groups : g.tiles_m;
   const int zs = g.kchunk ? (int)ceil_div(g.K, g.kchunk) : 1;
   const dim3 grid(entries * g.tiles_n, batch, zs), block(NT);
-#define NSH_GEMM(TA_, TB_, V_) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_>), grid, block, 0, s, g)
+  const bool plain = !g.c_rows && !g.row_scale && g.mode == kEpiAct;
+#define NSH_GEMM(TA_, TB_, V_)                                                                  \
+  do {                                                                                         \
+    if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true>), grid, block, 0, s, g);  \
+    else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false>), grid, block, 0, s, g);       \
+  } while (0)
   if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
   else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
   else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
