@@ -84,6 +84,43 @@ __device__ __forceinline__ T wave_max(T v) {
   return v;
 }
 
+// Lane exchange inside each 16-lane row of a wave through DPP (no LDS round
+// trip).  CTRL: 0xB1 = quad_perm [1,0,3,2] (lane ^ 1), 0x4E = quad_perm
+// [2,3,0,1] (lane ^ 2), 0x141 = row_half_mirror (lane i <-> 7 - i in each 8),
+// 0x140 = row_mirror (lane i <-> 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets the
+// same bits (each step adds two equal-valued partials in either order).
+__device__ __forceinline__ float group8_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v;
+}
+
+// Sum over each 16-lane row.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = group8_sum(v);
+  return v + dpp_mov<0x140>(v);
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Global-address-space views: loads through a pointer fetched from memory
+// (not a kernel argument) otherwise compile to flat accesses, which share
+// the LDS wait counter and serialise against every LDS exchange.
+typedef float fvec4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) fvec4 gfloat4;
+__device__ __forceinline__ gfloat* as_global(float* p) { return (gfloat*)p; }
+__device__ __forceinline__ const gfloat* as_global(const float* p) { return (const gfloat*)p; }
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace nship

@@ -17,11 +17,13 @@
 // vector receives the same projections in the same order as in the
 // reference's loop (q_0, q_1, ... q_{c-1}, then its own normalisation
 // v / (|v| + 1e-30)); only the order inside each dot product differs (per
-// thread partial sums, then a fixed tree).  One launch per panel: launch p
-// applies the projections of panel p to every later vector, kPB vectors per
-// workgroup held in registers, and the workgroup that owns panel p+1 then
-// factorizes it in registers and stores its normalised q vectors.  All Muon
-// matrices of the step advance together in the same launches.  Vectors live
+// thread partial sums, then a fixed tree of DPP row sums and one LDS
+// exchange).  One launch per panel: launch p applies the projections of
+// panel p to every later vector, kPB vectors per workgroup held in
+// registers, and the workgroup that owns panel p+1 then factorizes it in
+// registers and stores its normalised q vectors.  All Muon matrices of the
+// step advance together in the same launches; each workgroup spreads its
+// vectors over the 1024 threads according to its own matrix's length.  Vectors live
 // contiguously in a work buffer T[C][R] (a transpose of g when r >= c).
 // Vectors longer than kMaxPanelR take the per-column path (one launch per
 // column, every workgroup recomputing |v_j| with the same tree).
@@ -63,18 +65,29 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// T = the vectors of g, contiguous: r < c, the rows (a copy); r >= c, the
+// columns, T[j][k] = g[k][j], transposed in 32 x 32 tiles through LDS so both
+// sides are read and written along rows.  grid.y = matrix.
 __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restrict__ mats, int nmat) {
-  // grid.y = matrix; each thread copies one element of g into T (vector-major)
+  __shared__ float tile[32][33];
   const MuonMat& M = mats[blockIdx.y];
-  const int64_t n = (int64_t)M.R * M.C;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    // T[j][k]: vector j, element k
-    if (M.transposed) {
-      M.T[i] = M.g[i];  // rows of g are the vectors
-    } else {
-      const int64_t j = i / M.R, k = i % M.R;  // g[k][j], g is [R][C]
-      M.T[i] = M.g[k * M.C + j];
-    }
+  const gfloat* __restrict__ g = as_global(M.g);
+  gfloat* __restrict__ T = as_global(M.T);
+  const int64_t R = M.R, C = M.C;
+  if (M.transposed) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256) T[i] = g[i];
+    return;
+  }
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t tc = (C + 31) / 32, tiles = ((R + 31) / 32) * tc;
+  for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
+    const int64_t k0 = (b / tc) * 32, j0 = (b % tc) * 32;
+    for (int r = ty; r < 32; r += 8)
+      if (k0 + r < R && j0 + tx < C) tile[r][tx] = g[(k0 + r) * C + j0 + tx];
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8)
+      if (j0 + r < C && k0 + tx < R) T[(j0 + r) * R + k0 + tx] = tile[tx][r];
+    __syncthreads();
   }
   (void)nmat;
 }
@@ -115,46 +128,56 @@ __global__ __launch_bounds__(256) void mgs_normalize_kernel(const MuonMat* __res
 }
 
 // Sums NV values over the 1024 threads of a workgroup; every thread gets the
-// totals, identical in every lane.  Wave partials go to LDS; each wave then
-// re-reduces them with G = 64/NV lanes per value (fixed order) and broadcasts.
-// `red` alternates between two buffers in consecutive calls, so one barrier
-// per call suffices: a thread reads buffer b only before it reaches the
-// barrier of the next call, and buffer b is written again only after it.
+// totals as wave-uniform values.  Each 16-lane row sums through DPP and
+// stores one partial per value (64 partials: 16 waves x 4 rows); after the
+// barrier every wave re-reduces them, G = 64 / NV lanes per value reading NV
+// partials each, a DPP tree over the G lanes, and the totals are read out of
+// fixed lanes.  The order is fixed, so every workgroup and every call sums
+// the same way.  `red` alternates between two buffers in consecutive calls,
+// so one barrier per call suffices: a thread reads buffer b only before it
+// reaches the barrier of the next call, and buffer b is written again only
+// after it.
 template <int NV>
 __device__ __forceinline__ void panel_sum(float (&v)[NV], float* red) {
-  static_assert(64 % NV == 0 && 64 / NV <= 64, "NV must divide 64");
+  static_assert(kPanelWaves * 4 == 64 && (NV == 1 || NV == 2 || NV == 4 || NV == 8), "64 partials, NV | 8");
   constexpr int G = 64 / NV;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < NV; i++) v[i] = wave_sum(v[i]);
-  if (lane == 0) {
+  for (int i = 0; i < NV; i++) v[i] = row16_sum(v[i]);
+  const int i = lane & 15;
+  float s = v[0];
 #pragma unroll
-    for (int i = 0; i < NV; i++) red[w * NV + i] = v[i];
-  }
+  for (int k = 1; k < NV; k++)
+    if (i == k) s = v[k];
+  if (i < NV) red[(4 * w + (lane >> 4)) * NV + i] = s;
   __syncthreads();
-  const int i = lane / G, u0 = lane % G;
+  const int k = lane / G, u = lane % G;
   float p = 0.f;
 #pragma unroll
-  for (int u = 0; u < kPanelWaves; u += G)
-    if (u + u0 < kPanelWaves) p += red[(u + u0) * NV + i];
+  for (int j = 0; j < NV; j++) p += red[(u + G * j) * NV + k];
+  p = group8_sum(p);
+  if constexpr (G >= 16) p += dpp_mov<0x140>(p);
 #pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
+  for (int kk = 0; kk < NV; kk++) {
+    float t = read_lane(p, kk * G);
 #pragma unroll
-  for (int k = 0; k < NV; k++) v[k] = __shfl(p, k * G, 64);
+    for (int r = 1; r < G / 16; r++) t += read_lane(p, kk * G + 16 * r);
+    v[kk] = t;
+  }
 }
 
 // Elements of a vector held by thread t: VEC (R % 4 == 0, rows 16-byte
 // aligned): float4 chunks t + kPanelThreads * i, i < EPT / 4; otherwise
 // elements t + kPanelThreads * e.  Either way a wave's access is contiguous.
 template <int EPT, bool VEC>
-__device__ __forceinline__ void row_load(const float* __restrict__ row, int R, int t, bool valid,
+__device__ __forceinline__ void row_load(const gfloat* __restrict__ row, int R, int t, bool valid,
                                          float (&x)[EPT]) {
   if constexpr (VEC) {
 #pragma unroll
     for (int i = 0; i < EPT / 4; i++) {
       const int c = 4 * (t + kPanelThreads * i);
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (valid && c < R) v = *reinterpret_cast<const float4*>(row + c);
+      fvec4 v = {0.f, 0.f, 0.f, 0.f};
+      if (valid && c < R) v = *reinterpret_cast<const gfloat4*>(row + c);
       x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
     }
   } else {
@@ -167,12 +190,12 @@ __device__ __forceinline__ void row_load(const float* __restrict__ row, int R, i
 }
 
 template <int EPT, bool VEC>
-__device__ __forceinline__ void row_store(float* __restrict__ row, int R, int t, const float (&x)[EPT]) {
+__device__ __forceinline__ void row_store(gfloat* __restrict__ row, int R, int t, const float (&x)[EPT]) {
   if constexpr (VEC) {
 #pragma unroll
     for (int i = 0; i < EPT / 4; i++) {
       const int c = 4 * (t + kPanelThreads * i);
-      if (c < R) *reinterpret_cast<float4*>(row + c) = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
+      if (c < R) *reinterpret_cast<gfloat4*>(row + c) = fvec4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
     }
   } else {
 #pragma unroll
@@ -183,13 +206,121 @@ __device__ __forceinline__ void row_store(float* __restrict__ row, int R, int t,
   }
 }
 
+// Applies the kPB projections of the panel starting at vector q0 to the NV
+// vectors held in x, in order; q_{jj+1} is fetched while q_jj's projections
+// reduce.
+template <int EPT, bool VEC, int NV>
+__device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R, int q0, float (&x)[NV][EPT],
+                                            float (*red)[64 * kPB], int& par) {
+  const int t = threadIdx.x;
+  float qn[EPT];
+  row_load<EPT, VEC>(T + (int64_t)q0 * R, R, t, true, qn);
+#pragma unroll 1
+  for (int jj = 0; jj < kPB; jj++) {
+    float qv[EPT];
+#pragma unroll
+    for (int e = 0; e < EPT; e++) qv[e] = qn[e];
+    row_load<EPT, VEC>(T + (int64_t)(q0 + jj + 1) * R, R, t, jj + 1 < kPB, qn);
+    float d[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      d[v] = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPT; e++) d[v] += qv[e] * x[v][e];
+    }
+    panel_sum<NV>(d, red[par]);
+    par ^= 1;
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+      for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * qv[e];
+  }
+}
+
+// MGS inside a panel of nv vectors held in x that already carry every
+// earlier projection: normalise v_jj, project it out of the later vectors of
+// the panel, in order.
+template <int EPT>
+__device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (*red)[64 * kPB], int& par) {
+#pragma unroll
+  for (int jj = 0; jj < kPB; jj++) {
+    if (jj >= nv) break;
+    float s[1] = {0.f};
+#pragma unroll
+    for (int e = 0; e < EPT; e++) s[0] += x[jj][e] * x[jj][e];
+    panel_sum<1>(s, red[par]);
+    par ^= 1;
+    const float nrm = sqrtf(s[0]) + 1e-30f;
+#pragma unroll
+    for (int e = 0; e < EPT; e++) x[jj][e] /= nrm;
+    if (jj + 1 >= nv) break;
+    float d[kPB];
+#pragma unroll
+    for (int v = 0; v < kPB; v++) {
+      d[v] = 0.f;
+      if (v > jj) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) d[v] += x[jj][e] * x[v][e];
+      }
+    }
+    panel_sum<kPB>(d, red[par]);
+    par ^= 1;
+#pragma unroll
+    for (int v = 0; v < kPB; v++)
+      if (v > jj) {
+#pragma unroll
+        for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * x[jj][e];
+      }
+  }
+}
+
+// Elements per thread for a vector of length R (R <= kMaxPanelR).
+__device__ __forceinline__ int panel_ept(int R) {
+  return R <= kPanelThreads ? 1 : R <= 2 * kPanelThreads ? 2 : R <= 4 * kPanelThreads ? 4 : 8;
+}
+
+// Runs CALL with constexpr E (elements per thread) and V (float4 rows) set
+// for matrix M's vector length and alignment.
+#define NSH_WITH_LAYOUT(M, CALL)                                                             \
+  do {                                                                                       \
+    const bool vec_ = (M).R % 4 == 0 && (reinterpret_cast<uintptr_t>((M).T) & 15) == 0;     \
+    switch (panel_ept((M).R)) {                                                              \
+      case 1: { constexpr int E = 1; constexpr bool V = false; CALL; } break;               \
+      case 2: { constexpr int E = 2; constexpr bool V = false; CALL; } break;               \
+      case 4:                                                                                \
+        if (vec_) { constexpr int E = 4; constexpr bool V = true; CALL; }                   \
+        else { constexpr int E = 4; constexpr bool V = false; CALL; }                       \
+        break;                                                                               \
+      default:                                                                               \
+        if (vec_) { constexpr int E = 8; constexpr bool V = true; CALL; }                   \
+        else { constexpr int E = 8; constexpr bool V = false; CALL; }                       \
+        break;                                                                               \
+    }                                                                                        \
+  } while (0)
+
+// One workgroup's share of launch jp: project panel jp (jp >= 0) out of the
+// nv vectors c0 ..., and, for the lead workgroup (whose vectors are panel
+// jp + 1), factorize them.
+template <int EPT, bool VEC>
+__device__ __forceinline__ void mgs_panel_body(gfloat* __restrict__ T, int R, int jp, int c0, int nv, bool lead,
+                                               float (*red)[64 * kPB]) {
+  const int t = threadIdx.x;
+  float x[kPB][EPT];
+#pragma unroll
+  for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, v < nv, x[v]);
+  int par = 0;
+  if (jp >= 0) mgs_project<EPT, VEC, kPB>(T, R, jp, x, red, par);
+  if (lead) mgs_factor<EPT>(x, nv, red, par);
+#pragma unroll
+  for (int v = 0; v < kPB; v++)
+    if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, x[v]);
+}
+
 // Launch for panel jp (jp < 0: the first launch, no projections): vectors
 // c >= jp + kPB, kPB per workgroup; workgroup 0 of each matrix owns the next
-// panel and factorizes it.
-template <int EPT, bool VEC>
-__global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat* __restrict__ mats, int nmat,
-                                                                   int jp) {
-  __shared__ float red[2][kPanelWaves * kPB];
+// panel and factorizes it.  Each workgroup uses its own matrix's layout.
+__global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat* __restrict__ mats, int nmat, int jp) {
+  __shared__ float red[2][64 * kPB];
   const int first = jp + kPB;
   int b = blockIdx.x, mi = 0;
   for (; mi < nmat; mi++) {
@@ -200,89 +331,44 @@ __global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat*
   }
   if (mi >= nmat) return;
   const MuonMat& M = mats[mi];
-  const int R = M.R;
   const int c0 = first + b * kPB;
   const int nv = min(kPB, M.C - c0);
-  const int t = threadIdx.x;
-  float* __restrict__ T = M.T;
-  float x[kPB][EPT];
-#pragma unroll
-  for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, v < nv, x[v]);
-  int par = 0;
-  if (jp >= 0) {
-    // q_{jj+1} is fetched while q_jj's projections reduce.
-    float qn[EPT];
-    row_load<EPT, VEC>(T + (int64_t)jp * R, R, t, true, qn);
-#pragma unroll 1
-    for (int jj = 0; jj < kPB; jj++) {
-      float qv[EPT];
-#pragma unroll
-      for (int e = 0; e < EPT; e++) qv[e] = qn[e];
-      row_load<EPT, VEC>(T + (int64_t)(jp + jj + 1) * R, R, t, jj + 1 < kPB, qn);
-      float d[kPB];
-#pragma unroll
-      for (int v = 0; v < kPB; v++) {
-        d[v] = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPT; e++) d[v] += qv[e] * x[v][e];
-      }
-      panel_sum<kPB>(d, red[par]);
-      par ^= 1;
-#pragma unroll
-      for (int v = 0; v < kPB; v++)
-#pragma unroll
-        for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * qv[e];
-    }
-  }
-  if (b == 0) {
-#pragma unroll
-    for (int jj = 0; jj < kPB; jj++) {
-      if (jj >= nv) break;
-      float s[1] = {0.f};
-#pragma unroll
-      for (int e = 0; e < EPT; e++) s[0] += x[jj][e] * x[jj][e];
-      panel_sum<1>(s, red[par]);
-      par ^= 1;
-      const float nrm = sqrtf(s[0]) + 1e-30f;
-#pragma unroll
-      for (int e = 0; e < EPT; e++) x[jj][e] /= nrm;
-      float d[kPB];
-#pragma unroll
-      for (int v = 0; v < kPB; v++) {
-        d[v] = 0.f;
-        if (v > jj) {
-#pragma unroll
-          for (int e = 0; e < EPT; e++) d[v] += x[jj][e] * x[v][e];
-        }
-      }
-      panel_sum<kPB>(d, red[par]);
-      par ^= 1;
-#pragma unroll
-      for (int v = 0; v < kPB; v++)
-        if (v > jj) {
-#pragma unroll
-          for (int e = 0; e < EPT; e++) x[v][e] -= d[v] * x[jj][e];
-        }
-    }
-  }
-#pragma unroll
-  for (int v = 0; v < kPB; v++)
-    if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, x[v]);
+  gfloat* T = as_global(M.T);
+  const int R = M.R;
+  NSH_WITH_LAYOUT(M, (mgs_panel_body<E, V>(T, R, jp, c0, nv, b == 0, red)));
 }
 
-// w -= le * q + (0.01 lr) * w, q = T (normalised vectors).
+// w -= le * q + (0.01 lr) * w, q = T (normalised vectors): element [k][j]
+// of w takes q_j[k] (r >= c, through 32 x 32 LDS tiles) or q_k[j] (r < c).
 __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restrict__ mats, int nmat) {
 #pragma clang fp contract(off)
+  __shared__ float tile[32][33];
   const MuonMat& M = mats[blockIdx.y];
-  const int64_t n = (int64_t)M.R * M.C;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    // element i of w ([r][c] row-major) -> vector j, position k
-    int64_t j, k;
-    if (M.transposed) { j = i / M.R; k = i % M.R; }
-    else { k = i / M.C; j = i % M.C; }
-    const float q = M.T[j * M.R + k];
-    const float wi = M.w[i];
-    M.w[i] = wi - (M.le * q + M.decay * wi);
+  const gfloat* __restrict__ T = as_global(M.T);
+  gfloat* __restrict__ w = as_global(M.w);
+  const int64_t R = M.R, C = M.C;
+  const float le = M.le, decay = M.decay;
+  if (M.transposed) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256) {
+      const float wi = w[i];
+      w[i] = wi - (le * T[i] + decay * wi);
+    }
+    return;
+  }
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int64_t tr = (R + 31) / 32, tiles = tr * ((C + 31) / 32);
+  for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
+    const int64_t j0 = (b / tr) * 32, k0 = (b % tr) * 32;
+    for (int r = ty; r < 32; r += 8)
+      if (j0 + r < C && k0 + tx < R) tile[r][tx] = T[(j0 + r) * R + k0 + tx];
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8)
+      if (k0 + r < R && j0 + tx < C) {
+        const int64_t i = (k0 + r) * C + j0 + tx;
+        const float wi = w[i];
+        w[i] = wi - (le * tile[tx][r] + decay * wi);
+      }
+    __syncthreads();
   }
   (void)nmat;
 }
@@ -301,7 +387,7 @@ int muon_blocks(int C) { return (int)ceil_div(C, kCPB) > 0 ? (int)ceil_div(C, kC
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
-  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 256), 2048);
+  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 1024), 4096);
   hipLaunchKernelGGL(muon_gather_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
   NSH_LAUNCHED();
   return 0;
@@ -327,25 +413,13 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
     NSH_LAUNCHED();
     return 0;
   }
-  const int ept = max_r <= kPanelThreads ? 1 : max_r <= 2 * kPanelThreads ? 2 : max_r <= 4 * kPanelThreads ? 4 : 8;
-  bool vec = ept >= 4;
-  for (int i = 0; i < nmat; i++)
-    vec = vec && h_mats[i].R % 4 == 0 && (reinterpret_cast<uintptr_t>(h_mats[i].T) & 15) == 0;
   for (int jp = -kPB; jp + kPB < max_c; jp += kPB) {
     int grid = 0;
     for (int i = 0; i < nmat; i++) {
       const int nvec = h_mats[i].C - (jp + kPB);
       if (nvec > 0) grid += jp < 0 ? 1 : (int)ceil_div(nvec, kPB);
     }
-#define NSH_PANEL(E_, V_) \
-  hipLaunchKernelGGL((mgs_panel_kernel<E_, V_>), dim3(grid), dim3(kPanelThreads), 0, s, d_mats, nmat, jp)
-    switch (ept) {
-      case 1: NSH_PANEL(1, false); break;
-      case 2: NSH_PANEL(2, false); break;
-      case 4: if (vec) NSH_PANEL(4, true); else NSH_PANEL(4, false); break;
-      default: if (vec) NSH_PANEL(8, true); else NSH_PANEL(8, false); break;
-    }
-#undef NSH_PANEL
+    hipLaunchKernelGGL(mgs_panel_kernel, dim3(grid), dim3(kPanelThreads), 0, s, d_mats, nmat, jp);
     NSH_LAUNCHED();
   }
   return 0;
@@ -353,7 +427,7 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
 
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
-  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 256), 2048);
+  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 1024), 4096);
   hipLaunchKernelGGL(muon_update_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
   NSH_LAUNCHED();
   return 0;
