@@ -107,12 +107,13 @@ DOMINANT = {"c3": ("attention_fwd", "flash_fwd_kernel<64>", "mfma"),
 def roofline_of(key, region, work, ms_per_call):
     """Roofline object of the dominant kernel: algorithmic FLOP of one call
     over the HIP-event time of that call (profile region on the model's
-    stream); traffic not measured for these configs."""
+    stream); traffic = HBM bytes per call from rocprofv3 FETCH_SIZE /
+    WRITE_SIZE (profiles/)."""
     _, kernel, bound = DOMINANT[key]
     achieved = work / (ms_per_call * 1e-3) / 1e12
     return {"bound": bound, "kernel": kernel, "region": region, "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "flop_per_launch": work,
-            "avg_launch_ms": ms_per_call, "traffic": None}
+            "avg_launch_ms": ms_per_call, "traffic": load_traffic(f"{key}:{region}")}
 
 
 def routing_report(best, logits, E):
@@ -296,20 +297,38 @@ def bench_c2(steps, warmup, with_cpu):
     return res
 
 
+def copy_calibration():
+    """A plain copy of known size for calibrating rocprofv3's FETCH_SIZE /
+    WRITE_SIZE counters: the embedding gather with identity ids copies a
+    65536 x 1024 fp32 table (256 MiB read, 256 MiB written), three launches."""
+    from neuralscript_amd import runtime
+    V, D = 65536, 1024
+    W = runtime.DeviceArray(V * D)
+    out = runtime.DeviceArray(V * D)
+    idx = runtime.DeviceArray.from_host(np.arange(V, dtype=np.float32))
+    for _ in range(3):
+        runtime.op("embedding", W, idx, out, V, V, D)
+    runtime.check(runtime.lib().nsh_device_synchronize(), "synchronize")
+    return {"calibration": "embedding identity copy", "bytes_read": V * D * 4, "bytes_written": V * D * 4,
+            "launches": 3}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"],
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "copy"],
                     help="c2 (default) is the metric's workload; c3/c4 (forward) and c5 (training steps) "
-                         "print per-kernel breakdowns")
+                         "print per-kernel breakdowns; copy runs the rocprof counter calibration copy")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
         raise SystemExit("bench.py: this build measures one GPU only (single-GPU boxes; "
                          "see DESIGN.md for how the path would shard)")
-    if a.config == "c2":
+    if a.config == "copy":
+        res = copy_calibration()
+    elif a.config == "c2":
         res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
     elif a.config == "c5":
         res = bench_train(a.config, a.steps, a.warmup)
