@@ -122,6 +122,8 @@ int launch_index(const float* in, const int64_t* idx, float* out, int64_t M, int
 int launch_scatter(const float* in, const int64_t* idx, const float* upd, float* out, int64_t R, int64_t C,
                    int64_t L, int axis, hipStream_t s);
 int launch_fill(float* out, int64_t n, float v, hipStream_t s);
+// y = x * (keep[i] ? scale : 0): a dropout's forward (train mode) and its gradient
+int launch_dropout(const float* x, const uint8_t* keep, float* y, int64_t n, float scale, hipStream_t s);
 int launch_copy(const float* in, float* out, int64_t n, hipStream_t s);
 
 // moe.hip ----------------------------------------------------------------------

@@ -8,6 +8,7 @@
 //   slice      ns_slice2/rows  codegen.cpp:1663-1676
 //   index      ns_index2/rows  codegen.cpp:1678-1691
 //   scatter    ns_scatter2/rows codegen.cpp:1693-1709 (later indices win)
+//   dropout    train-mode mask apply, codegen.cpp:2874-2893, :3066-3073
 //
 // All are HBM-bound copies or single-pass elementwise work; the launchers
 // assume the host has checked every index against its buffer.
@@ -122,6 +123,16 @@ __global__ __launch_bounds__(256) void scatter_kernel(const float* __restrict__ 
   else out[i] = axis == 1 ? upd[r * L + hit] : upd[hit * C + c];
 }
 
+// y = x * m, m = keep ? scale : 0 (codegen.cpp:2887 forward, :3066-3073
+// backward with the same mask).
+__global__ __launch_bounds__(256) void dropout_kernel(const float* __restrict__ x, const uint8_t* __restrict__ keep,
+                                                      float* __restrict__ y, int64_t n, float scale) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float m = keep[i] ? scale : 0.f;
+  y[i] = x[i] * m;
+}
+
 __global__ void fill_kernel(float* __restrict__ out, int64_t n, float v) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) out[i] = v;
@@ -191,6 +202,13 @@ int launch_scatter(const float* in, const int64_t* idx, const float* upd, float*
                    int64_t L, int axis, hipStream_t s) {
   if (R * C <= 0) return 0;
   hipLaunchKernelGGL(scatter_kernel, dim3(blocks(R * C)), dim3(256), 0, s, in, idx, upd, out, R, C, L, axis);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+int launch_dropout(const float* x, const uint8_t* keep, float* y, int64_t n, float scale, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(dropout_kernel, dim3(blocks(n)), dim3(256), 0, s, x, keep, y, n, scale);
   NSH_LAUNCHED();
   return 0;
 }

@@ -265,7 +265,11 @@ Plan* parse_plan(const char* text, std::string* err) {
         I.act = act_code(o.substr(14));
         if (I.act < 0) { *err = "unsupported activation: " + o; return false; }
       }
-      else if (o == "ns.dropout") I.op = Op::Dropout;
+      else if (o == "ns.dropout") {
+        I.op = Op::Dropout;
+        const std::string v = comment_str(r.comment, "rate");
+        I.rate = v.empty() ? 0.0 : std::strtod(v.c_str(), nullptr);
+      }
       else if (o == "ns.layernorm") I.op = Op::LayerNorm;
       else if (o == "ns.layer.embedding") I.op = Op::Embedding;
       else if (o == "ns.layer.attention") I.op = Op::Attention;
@@ -275,11 +279,10 @@ Plan* parse_plan(const char* text, std::string* err) {
       else if (o == "ns.grad.matmul.a") I.op = Op::MatmulGradA;
       else if (o == "ns.grad.matmul.w") I.op = Op::MatmulGradW;
       else if (o == "ns.grad.activation") {
-        if (r.comment.find("dropout") != std::string::npos) {
-          *err = "dropout in training is not supported (the reference draws its mask from mt19937)";
-          return false;
-        }
+        // a dropout's gradient multiplies by the saved mask
+        // (mlir_compiler.cpp:362-375: operand 1 is the dropout's result)
         I.op = Op::ActGrad;
+        I.dropout = r.comment.find("dropout_mask") != std::string::npos;
       }
       else if (o == "ns.grad.layernorm") I.op = Op::LayerNormGrad;
       else if (o == "ns.grad.embedding.w") I.op = Op::EmbeddingGradW;
@@ -358,7 +361,12 @@ Plan* parse_plan(const char* text, std::string* err) {
           if (J.op == Op::Attention && J.in[1] == I.in[2]) { I.heads = J.heads; found = true; }
         if (!found) { *err = "attention grad without its forward"; return false; }
       }
-      if (I.op == Op::ActGrad) {
+      if (I.op == Op::ActGrad && I.dropout) {
+        bool found = false;
+        for (auto& J : F->ins)
+          if (J.op == Op::Dropout && J.res == I.in[1]) { I.rate = J.rate; found = true; }
+        if (!found) { *err = "dropout grad without its forward"; return false; }
+      } else if (I.op == Op::ActGrad) {
         bool found = false;
         for (auto& J : F->ins) {
           if (J.op == Op::Act && J.in[0] == I.in[1]) { I.act = J.act; found = true; }

@@ -2,7 +2,7 @@
 // /root/reference/src/mlir/mlir_compiler.cpp:949-1025), resolved into value
 // ids, weight offsets and per-op attributes.  Attributes that printer drops
 // arrive as key=value tokens in the instruction comment (initial=, op=,
-// value=, axis=, start=, stop=, idx=).  Pure host code.
+// value=, axis=, start=, stop=, idx=, rate=).  Pure host code.
 #pragma once
 #include <cstdint>
 #include <map>
@@ -41,6 +41,8 @@ struct Instr {
   int64_t start = 0, stop = 0;  // Slice
   std::vector<int64_t> idx;   // Index / Scatter
   float value = 0.f;          // Constant
+  double rate = 0.0;          // Dropout: float_attr; ActGrad of a dropout: that dropout's
+  bool dropout = false;       // ActGrad: the gradient of a dropout (dIn = dOut * its mask)
 };
 
 struct Value {

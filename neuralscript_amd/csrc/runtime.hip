@@ -60,6 +60,7 @@ struct ns_model {
   size_t moe_count = 0;
   uint8_t* d_active = nullptr;
   std::mt19937 rng{0x9E3779B9u};  // codegen.cpp:2421
+  std::map<int, std::vector<uint8_t>> drop_keep;  // host staging of each dropout's keep flags
   int64_t lr_step = 0;
   int64_t moe_last_m = 0;         // tokens routed by the last MoE forward
   struct Adam {
@@ -160,6 +161,7 @@ struct Frame {
   std::vector<size_t> numel;
   std::vector<float*> ptr;
   std::map<int, AttnSaved> attn;  // keyed by the attention input value id
+  bool backward = false;          // train_mode: a backward pass and optimizer step follow
 };
 
 float* scratch(ns_model* m, const std::string& key, size_t n) {
@@ -244,6 +246,22 @@ float* out_buf(ns_model* m, Frame& fr, int id, size_t n) {
   if (!var) return -1
 
 // Forward instructions (shared by inference and the training forward).
+// A dropout's rate as the emitted code spells it: clamped to [0, 0.999999]
+// and printed with std::to_string into the source (codegen.cpp:2877-2880).
+double dropout_rate(double rate) {
+  if (rate < 0.0) rate = 0.0;
+  if (rate >= 1.0) rate = 0.999999;
+  return std::strtod(std::to_string(rate).c_str(), nullptr);
+}
+
+float dropout_scale(double r) { return 1.0f / (float)(1.0 - r); }
+
+// Device keep flags (one byte per element) of the dropout whose result is `res`.
+uint8_t* drop_mask(ns_model* m, int res, size_t n) {
+  float* p = scratch(m, "dropmask" + std::to_string(res), (n + 3) / 4);
+  return reinterpret_cast<uint8_t*>(p);
+}
+
 int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool train) {
   const Plan& P = *m->plan;
   hipStream_t s = m->stream;
@@ -473,14 +491,28 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       return launch_scatter(fr.ptr[I.in[0]], d, fr.ptr[I.in[1]], y, I.axis == 1 ? M : R, C, L, I.axis == 1 ? 1 : 0,
                             s);
     }
-    case Op::Dropout:
-      if (train) {
-        set_error("dropout in training is not supported");
-        return -1;
+    case Op::Dropout: {
+      const size_t n = fr.numel[I.in[0]];
+      if (!(train && fr.backward)) {  // inference and objective: a copy (codegen.cpp:1999-2005, :2888-2890)
+        fr.numel[I.res] = n;
+        fr.ptr[I.res] = fr.ptr[I.in[0]];
+        return 0;
       }
-      fr.numel[I.res] = fr.numel[I.in[0]];
-      fr.ptr[I.res] = fr.ptr[I.in[0]];
-      return 0;
+      // codegen.cpp:2874-2893: keep ~ bernoulli(1 - r) from the context's
+      // mt19937, one draw per element in order, on the host exactly as the
+      // reference draws it; the device applies m = keep ? 1/(1-r) : 0.
+      const double r = dropout_rate(I.rate);
+      std::bernoulli_distribution keep(1.0 - r);
+      std::vector<uint8_t>& hk = m->drop_keep[I.res];
+      hk.resize(n);
+      for (size_t i = 0; i < n; i++) hk[i] = keep(m->rng) ? 1 : 0;
+      uint8_t* dk = drop_mask(m, I.res, n);
+      if (!dk) return -1;
+      if (n) NSH_CHECK(hipMemcpyAsync(dk, hk.data(), n, hipMemcpyHostToDevice, s));
+      NSH_OUT(y, I.res, n);
+      Prof p(m, "dropout");
+      return launch_dropout(fr.ptr[I.in[0]], dk, y, (int64_t)n, dropout_scale(r), s);
+    }
     default:
       break;
   }
@@ -661,6 +693,14 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
   return muon_batch(d, m->muon_host, max_elems, s);
 }
 
+// Class count of CROSS_ENTROPY / LOSS_GRAD: the logits' static columns
+// (result type or weight shape), else the input width, not the propagated
+// width (codegen.cpp:2896, :2904); rows = numel / C.
+int64_t ce_classes(const Func& F, const Plan& P, int preds) {
+  const int64_t c = preds < (int)F.scols.size() ? F.scols[preds] : -1;
+  return c > 0 ? c : P.in_cols;
+}
+
 int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, float lr, bool train_mode,
               float** d_loss) {
   const Plan& P = *m->plan;
@@ -668,6 +708,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
   hipStream_t s = m->stream;
   Frame fr;
   bind_weights(m, fr);
+  fr.backward = train_mode;
   fr.numel[F.x] = n_in;
   fr.ptr[F.x] = const_cast<float*>(d_x);
   float* loss = scratch(m, "loss", 1);
@@ -686,8 +727,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
         if (exec_forward_op(m, F, I, fr, true) != 0) return -1;
         break;
       case Op::CrossEntropy: {
-        // C = the logits' columns (codegen.cpp:2901-2906), rows = numel / C
-        int64_t C = F.width[I.in[0]] > 0 ? F.width[I.in[0]] : P.in_cols;
+        const int64_t C = ce_classes(F, P, I.in[0]);
         const size_t n = fr.numel[I.in[0]];
         const int64_t rows = (int64_t)(n / (size_t)C);
         fr.numel[F.y] = n;
@@ -708,13 +748,17 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
         }
         Prof p(m, "softmax_xent");
         if (launch_softmax_xent(fr.ptr[I.in[0]], d_y, grad, rl, loss, rows, C, grad != nullptr, s) != 0) return -1;
+        // ns_loss_grad leaves the elements past the last whole row unwritten:
+        // zeros in the freshly sized buffer (codegen.cpp:1582-1595)
+        if (grad && (size_t)(rows * C) < n && launch_fill(grad + rows * C, (int64_t)n - rows * C, 0.f, s) != 0)
+          return -1;
         break;
       }
       default:
         if (!train_mode) break;
         switch (I.op) {
           case Op::LossGrad: {
-            const int64_t C = F.width[I.in[0]] > 0 ? F.width[I.in[0]] : P.in_cols;
+            const int64_t C = ce_classes(F, P, I.in[0]);
             const size_t n = fr.numel[I.in[0]];
             const int64_t rows = (int64_t)(n / (size_t)C);
             NSH_OUT(grad, I.res, n);
@@ -723,6 +767,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             if (!rl || !tmp) return -1;
             Prof p(m, "softmax_xent");
             if (launch_softmax_xent(fr.ptr[I.in[0]], d_y, grad, rl, tmp, rows, C, true, s) != 0) return -1;
+            if ((size_t)(rows * C) < n && launch_fill(grad + rows * C, (int64_t)n - rows * C, 0.f, s) != 0) return -1;
             break;
           }
           case Op::MatmulGradA: {
@@ -736,7 +781,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             int res = I.res;
             if (ii + 1 < F.ins.size()) {
               const Instr& J = F.ins[ii + 1];
-              if (J.op == Op::ActGrad && J.in[0] == I.res && uses_of(F, I.res) == 1) {
+              if (J.op == Op::ActGrad && !J.dropout && J.in[0] == I.res && uses_of(F, I.res) == 1) {
                 g.mode = kEpiActGrad;
                 g.act = J.act;
                 g.aux = fr.ptr[J.in[1]];
@@ -763,6 +808,17 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
           case Op::ActGrad: {
             const size_t n = fr.numel[I.in[0]];
             NSH_OUT(y, I.res, n);
+            if (I.dropout) {  // dOut * the dropout's saved mask (codegen.cpp:3066-3073)
+              if (fr.numel[I.in[1]] != n) {
+                set_error("dropout grad: size differs from its forward");
+                return -1;
+              }
+              Prof p(m, "dropout");
+              if (launch_dropout(fr.ptr[I.in[0]], drop_mask(m, I.in[1], n), y, (int64_t)n,
+                                 dropout_scale(dropout_rate(I.rate)), s) != 0)
+                return -1;
+              break;
+            }
             Prof p(m, "act_grad");
             if (launch_act_grad(fr.ptr[I.in[0]], fr.ptr[I.in[1]], y, (int64_t)n, I.act, s) != 0) return -1;
             break;

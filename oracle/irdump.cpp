@@ -9,7 +9,7 @@
 //   ns.reshape         shape=<r>:<c>
 //   ns.slice           axis=<a> start=<s> stop=<e>
 //   ns.index/scatter   axis=<a> idx=<i0,i1,...>   (int_attr, ints_attr)
-//   ns.dropout         rate=<p>              (float_attr)
+//   ns.dropout         rate=<p>              (float_attr, 17 significant digits)
 //   ns.layer.moe       initial=<K0>          (ints_attr[0], mlir_compiler.cpp:896)
 //
 // libnship's plan parser reads these keys.  Test/build infrastructure only:
@@ -51,7 +51,14 @@ std::string attrs_of(const ns::MLIRInstr& in) {
       break;
     }
     case MLIROp::INDEX: case MLIROp::SCATTER: o << "axis=" << in.int_attr << " idx=" << ints(); break;
-    case MLIROp::DROPOUT: o << "rate=" << in.float_attr; break;
+    case MLIROp::DROPOUT: {
+      // exact value: the emitted code prints it with std::to_string
+      std::ostringstream r;
+      r.precision(17);
+      r << in.float_attr;
+      o << "rate=" << r.str();
+      break;
+    }
     case MLIROp::LAYER_MOE:
       if (!in.ints_attr.empty()) o << "initial=" << in.ints_attr[0];
       break;

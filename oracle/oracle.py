@@ -205,7 +205,9 @@ def cross_entropy(preds, labels, C):
 
 
 def loss_grad(preds, labels, C):
-    d = empty(preds.size)
+    # elements past the last whole row of C are never written by ns_loss_grad
+    # (codegen.cpp:1582-1595); its freshly resized buffer holds zeros there
+    d = np.zeros(preds.size, dtype=np.float32)
     lib().or_loss_grad(fp(preds), fp(labels), fp(d), preds.size, C)
     return d
 
@@ -506,6 +508,46 @@ class Net:
         return (input_numel // self.in_cols) * self.out_cols
 
 
+class MT19937:
+    """std::mt19937 (the reference context's RNG, codegen.cpp:2419-2421):
+    Matsumoto-Nishimura MT19937 with the standard's init_genrand seeding;
+    numpy's MT19937 core generates, its state is set from that seeding.
+    Pinned by the standard's check value (the 10000th draw of a default-
+    seeded engine is 4123659995, [rand.predef]) in tests/test_oracle.py."""
+
+    def __init__(self, seed):
+        key = np.zeros(624, dtype=np.uint64)
+        key[0] = seed & 0xFFFFFFFF
+        for i in range(1, 624):
+            prev = int(key[i - 1])
+            key[i] = (1812433253 * (prev ^ (prev >> 30)) + i) & 0xFFFFFFFF
+        self.bg = np.random.MT19937()
+        self.bg.state = {"bit_generator": "MT19937", "state": {"key": key.astype(np.uint32), "pos": 624}}
+
+    def draws(self, n):
+        return self.bg.random_raw(n).astype(np.uint64)
+
+
+def bernoulli(rng, n, p):
+    """n draws of libstdc++'s std::bernoulli_distribution(p)(rng): true iff
+    generate_canonical<double, 53>(rng) < p, where generate_canonical takes
+    two 32-bit draws d1, d2 and returns (d1 + d2 * 2^32) / 2^64 in double
+    arithmetic, clamped below 1 (bits/random.h, bits/random.tcc of the
+    libstdc++ the reference's driver is compiled against)."""
+    d = rng.draws(2 * n)
+    s = d[0::2].astype(np.float64) + d[1::2].astype(np.float64) * 4294967296.0
+    r = s / 18446744073709551616.0
+    r[r >= 1.0] = np.nextafter(1.0, 0.0)
+    return r < p
+
+
+def dropout_rate(rate):
+    """The rate as the emitted code spells it: clamped to [0, 0.999999] and
+    printed with std::to_string (codegen.cpp:2877-2880)."""
+    rate = 0.0 if rate < 0.0 else (0.999999 if rate >= 1.0 else rate)
+    return float("%f" % rate)
+
+
 def _act_of(f, pre):
     for i in f.instrs:
         if i.op.startswith("ns.activation.") and i.operands and i.operands[0] == pre:
@@ -540,6 +582,7 @@ class Model:
         self.net = net
         self.w = w.copy()
         self.lr_step = 0
+        self.rng = MT19937(0x9E3779B9)  # the context's engine, codegen.cpp:2421
         self.adam = {}  # name -> (m, v, t)
         self.active = None
         if net.moe:
@@ -556,6 +599,15 @@ class Model:
         net = self.net
         wset = set(net.shape)
         buf = {}
+        masks = {}  # dropout result id -> its scaled mask (train_mode forward)
+        static = net.ids_table(f) if f.is_train else {}
+
+        def ce_cols(preds):
+            # the class count of CROSS_ENTROPY / LOSS_GRAD: the logits' static
+            # cols (result type or weight shape), else the input width
+            # (codegen.cpp:2896, :2904), not the propagated width
+            c = static.get(preds, (-1, -1))[1]
+            return c if c > 0 else net.in_cols
         xid = _input_id(f, wset)
         yid = None
         for i in f.instrs:
@@ -717,9 +769,17 @@ class Model:
                 buf[i.result] = act(val(o[0]), ACT_CODES[kind])
                 width[i.result] = cols(o[0])
             elif op == "ns.dropout":
-                if train_mode:
-                    raise NotImplementedError("dropout in training draws from mt19937")
-                buf[i.result] = val(o[0]).copy()
+                src = val(o[0])
+                if f.is_train and train_mode:
+                    # codegen.cpp:2874-2893: m = keep ? 1/(1-r) : 0 per element, in order
+                    r = dropout_rate(float(comment_str(i.comment, "rate") or 0.0))
+                    scale = np.float32(1.0) / np.float32(1.0 - r)
+                    keep = bernoulli(self.rng, src.size, 1.0 - r)
+                    m = np.where(keep, scale, np.float32(0.0)).astype(np.float32)
+                    masks[i.result] = m
+                    buf[i.result] = (src * m).astype(np.float32)
+                else:
+                    buf[i.result] = src.copy()
                 width[i.result] = cols(o[0])
             elif op == "ns.layernorm":
                 src = val(o[0])
@@ -751,12 +811,11 @@ class Model:
                     record["moe_best"] = best
                     record["moe_prob"] = prob
             elif op == "ns.cross_entropy":
-                C = cols(o[0])
-                loss = cross_entropy(val(o[0]), y, C)
+                loss = cross_entropy(val(o[0]), y, ce_cols(o[0]))
             elif not train_mode:
                 continue
             elif op == "ns.grad.loss":
-                C = cols(o[0])
+                C = ce_cols(o[0])
                 buf[i.result] = loss_grad(val(o[0]), y, C)
                 width[i.result] = C
             elif op == "ns.grad.matmul.a":
@@ -771,6 +830,10 @@ class Model:
                 M = dC.size // N
                 buf[i.result] = matmul_grad_w(val(o[0]), dC, M, K, N)
                 grads[o[2]] = i.result
+            elif op == "ns.grad.activation" and o[1] in masks:
+                # dropout's gradient: dOut * the saved mask (codegen.cpp:3066-3073)
+                buf[i.result] = (val(o[0]) * masks[o[1]]).astype(np.float32)
+                width[i.result] = cols(o[0])
             elif op == "ns.grad.activation":
                 code = _act_of(f, o[1])
                 buf[i.result] = act_grad(val(o[0]), val(o[1]), code)

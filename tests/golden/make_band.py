@@ -10,7 +10,7 @@ Muon normalises the rounding noise of rank-deficient gradient directions
 much under a mere change of summation order; a GPU implementation is held to
 1e-3 plus a small multiple of this band.
 
-    python tests/golden/make_band.py
+    python tests/golden/make_band.py [net ...]    (default: every net)
 """
 import os
 import sys
@@ -44,9 +44,9 @@ def spread(run, ref):
     return out
 
 
-def main():
+def main(names=()):
     for name, rows, seed, steps, lr, _ in CASES:
-        if not steps:
+        if not steps or (names and name not in names):
             continue
         net, x, y = case_inputs(name, rows, seed)
 
@@ -59,6 +59,8 @@ def main():
         update(path, band=band)
         print(name, "band", band)
     for name, rows, seed, base in CURVES:
+        if names and name not in names:
+            continue
         net = oracle.Net(helpers.ir_text(name))
         x = helpers.net_inputs(net, name, seed, rows)
         y = helpers.net_labels(net, seed, rows)
@@ -74,4 +76,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

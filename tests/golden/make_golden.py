@@ -48,6 +48,7 @@ CASES = [
     ("bop", 41, 114, 0, 0.0, False),
     ("dmx", 23, 115, 0, 0.0, False),
     ("smt", 33, 116, 3, 0.05, False),
+    ("drp", 37, 117, 4, 0.05, False),
 ]
 
 
@@ -63,7 +64,8 @@ def case_inputs(name, rows, seed):
 # 100-step loss curves, host-side cosine warmup schedule (lr * lr_scale(t),
 # t = 0..99, so the first step has lr 0), on reduced c5 twins:
 # name, tokens, seed, base lr
-CURVES = [("c5s", 256, 201, 3e-4), ("c5s", 256, 202, 0.02), ("c5t", 96, 203, 0.05), ("moeb", 512, 204, 0.01)]
+CURVES = [("c5s", 256, 201, 3e-4), ("c5s", 256, 202, 0.02), ("c5t", 96, 203, 0.05), ("moeb", 512, 204, 0.01),
+          ("drp", 128, 205, 0.01)]
 
 
 def curve_lrs(base, steps=100):

@@ -46,7 +46,7 @@ def test_oracle_matches_reference_fixtures(case):
                     reason="reference build (oracle/_ref) not present")
 @pytest.mark.parametrize("name,rows", [("c2s", 41), ("c3s", 70), ("c4k", 64), ("c5t", 50), ("moet", 23), ("mlpt", 9),
                                        ("moeb", 37), ("dmv", 23), ("dmw", 31), ("bop", 19),
-                                       ("dmx", 17)])
+                                       ("dmx", 17), ("drp", 29), ("drp", 64)])
 def test_oracle_matches_reference_build(name, rows):
     from neuralscript_amd.abi import NsLib
     net = oracle.Net(helpers.ir_text(name))
@@ -68,6 +68,24 @@ def test_oracle_matches_reference_build(name, rows):
 
 
 # ---- closed forms ---------------------------------------------------------
+
+
+def test_mt19937_matches_the_standard_check_value():
+    """The dropout masks come from the context's std::mt19937: the C++
+    standard fixes the 10000th draw of a default-seeded (5489) engine at
+    4123659995 ([rand.predef]); the first draws are the published sequence."""
+    d = oracle.MT19937(5489).draws(10000)
+    assert int(d[-1]) == 4123659995
+    assert [int(v) for v in d[:3]] == [3499211612, 581869302, 3890346734]
+
+
+def test_bernoulli_keep_fraction_and_rate_spelling():
+    """bernoulli(p) keeps a fraction p of draws within 5 sigma, and the rate
+    is the emitted literal: clamped, printed with 6 decimals."""
+    k = oracle.bernoulli(oracle.MT19937(0x9E3779B9), 200000, 0.75)
+    assert abs(k.mean() - 0.75) <= 5 * np.sqrt(0.75 * 0.25 / k.size)
+    assert oracle.dropout_rate(0.1) == 0.1 and oracle.dropout_rate(0.1234567) == 0.123457
+    assert oracle.dropout_rate(-1.0) == 0.0 and oracle.dropout_rate(1.0) == 0.999999
 
 def test_layernorm_rows_are_standardised():
     x = synth.normal(1, 37 * 96, 3.0) + 5.0
