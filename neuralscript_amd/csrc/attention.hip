@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     const float mnew = fmaxf(m, mloc);
     if (__any(mnew > m)) {
-      const float corr = exp2f(m - mnew);
+      const float corr = exp2_hw(m - mnew);
       l *= corr;
 #pragma unroll
       for (int d = 0; d < NDB; d++)
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int v = 0; v < 16; v++) {
-        const float p = exp2f(sc[kb][v] - mnew);
+        const float p = exp2_hw(sc[kb][v] - mnew);
         sc[kb][v] = p;
         lsum += p;
       }
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int qr = qb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        const float p = key < S ? exp2f(sc[v] * c_log2 - ls[qr]) : 0.f;
+        const float p = key < S ? exp2_hw(sc[v] * c_log2 - ls[qr]) : 0.f;
         sc[v] = p;
         dp[v] = p * (dp[v] - ds[qr]);
       }
@@ -562,7 +562,7 @@ __global__ __launch_bounds__(256) void flash_bwd_dq_kernel(const float* __restri
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int kr = kbase + kb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        const float p = kr < S ? exp2f(sc[kb][v] * c_log2 - lq) : 0.f;
+        const float p = kr < S ? exp2_hw(sc[kb][v] * c_log2 - lq) : 0.f;
         dp[kb][v] = p * (dp[kb][v] - dq_delta);
       }
     // dQ^T += K^T dS^T: step s of key block kb pairs key 8(s/4) + 4kh + s%4.

@@ -108,6 +108,12 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_mov<0x140>(v);
 }
 
+// 2^x as the hardware's v_exp_f32 computes it (about 1 ulp; results below
+// 2^-126 flush to zero, where exp2f would produce the subnormal).  Used for
+// softmax probabilities, whose terms below 2^-126 of the row maximum change
+// no sum.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float read_lane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
