@@ -394,6 +394,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
   const int hcol = h * DK;
   const int64_t hS = (int64_t)h * S;
   const int key = k0 + w * 32 + l32;  // this lane's key (column of S)
+  const float kneg = key < S ? 0.f : -INFINITY;
 
   // B operands: K and V rows of this lane's key, head dims 8g + 4kh + (0..3).
   float kf[DK / 2], vf[DK / 2];
@@ -446,7 +447,9 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int qr = qb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        const float p = key < S ? exp2_hw(sc[v] * c_log2 - ls[qr]) : 0.f;
+        // keys past the end: exponent -inf (kneg), p = 0; lse is finite or
+        // +inf, so no NaN, and no per-element branch
+        const float p = exp2_hw(fmaf(sc[v], c_log2, kneg) - ls[qr]);
         sc[v] = p;
         dp[v] = p * (dp[v] - ds[qr]);
       }
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(256) void flash_bwd_dq_kernel(const float* __restri
 #pragma unroll
       for (int v = 0; v < 16; v++) {
         const int kr = kbase + kb * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        const float p = kr < S ? exp2_hw(sc[kb][v] * c_log2 - lq) : 0.f;
+        const float p = exp2_hw(fmaf(sc[kb][v], c_log2, kr < S ? 0.f : -INFINITY) - lq);
         dp[kb][v] = p * (dp[kb][v] - dq_delta);
       }
     // dQ^T += K^T dS^T: step s of key block kb pairs key 8(s/4) + 4kh + s%4.
