@@ -184,10 +184,13 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
     // Grouped: tile entry -> (group, m tile); rows [seg[e], seg[e+1]) of the
     // group, B advanced by e * sBg.  Entries run XCD-contiguously with all
     // their n tiles, so a gathered A tile is fetched into one XCD's L2 only.
-    // Surplus workgroups exit (uniformly).
-    const int L = xcd_linear(blockIdx.x, gridDim.x);
+    // The grid is an upper bound: the workgroups past the device-side tile
+    // count exit (uniformly), and the rest are spread over the 8 XCDs by
+    // that count, not by the grid size, so each XCD gets an equal share.
+    const int T = *g.ntiles * tiles_n;
+    if ((int)blockIdx.x >= T) return;
+    const int L = xcd_linear(blockIdx.x, T);
     const int entry = L / tiles_n;
-    if (entry >= *g.ntiles) return;
     const int e = g.tiles[2 * entry], mt = g.tiles[2 * entry + 1];
     m0 = g.seg[e] + mt * BM;
     m_end = g.seg[e + 1];
