@@ -240,6 +240,66 @@ __global__ __launch_bounds__(256) void softmax_xent_vec_kernel(const float* __re
   if (lane == 0) row_loss[r] = loss;
 }
 
+// One workgroup (256 threads) per row of up to 1024 * NV4 floats, the row
+// held in registers (NV4 float4 per thread): logits and labels are read
+// once.  Same per-element operations as the reference (max, expf(x - max),
+// sum, divide, -logf(p) where y > 0, (p - y) / rows); sums over a fixed tree.
+template <int NV4>
+__global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __restrict__ logits,
+                                                               const float* __restrict__ labels,
+                                                               float* __restrict__ grad, float* __restrict__ row_loss,
+                                                               int64_t rows, int64_t C, int write_grad) {
+  __shared__ float red[3][4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t r = blockIdx.x;
+  const int64_t C4 = C / 4;
+  const float4* xr = reinterpret_cast<const float4*>(logits + r * C);
+  const float4* yr = reinterpret_cast<const float4*>(labels + r * C);
+  float4 x[NV4], y[NV4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV4; i++) {
+    const int64_t c = t + 256 * i;
+    const bool in = c < C4;
+    x[i] = in ? xr[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    y[i] = in ? yr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    mx = fmaxf(mx, fmaxf(fmaxf(x[i].x, x[i].y), fmaxf(x[i].z, x[i].w)));
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[0][w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV4; i++) {
+    x[i] = make_float4(expf(x[i].x - mx), expf(x[i].y - mx), expf(x[i].z - mx), expf(x[i].w - mx));
+    s += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+  }
+  s = wave_sum(s);
+  if (lane == 0) red[1][w] = s;
+  __syncthreads();
+  s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  const float inv_rows = 1.f / (float)rows;
+  float4* gr = reinterpret_cast<float4*>(grad + r * C);
+  float loss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV4; i++) {
+    const int64_t c = t + 256 * i;
+    const float p0 = x[i].x / s, p1 = x[i].y / s, p2 = x[i].z / s, p3 = x[i].w / s;
+    if (y[i].x > 0.f) loss -= logf(p0);
+    if (y[i].y > 0.f) loss -= logf(p1);
+    if (y[i].z > 0.f) loss -= logf(p2);
+    if (y[i].w > 0.f) loss -= logf(p3);
+    if (write_grad && c < C4)
+      gr[c] = make_float4((p0 - y[i].x) * inv_rows, (p1 - y[i].y) * inv_rows, (p2 - y[i].z) * inv_rows,
+                          (p3 - y[i].w) * inv_rows);
+  }
+  loss = wave_sum(loss);
+  if (lane == 0) red[2][w] = loss;
+  __syncthreads();
+  if (t == 0) row_loss[r] = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+}
+
 // Deterministic single-workgroup sum of row losses / rows.
 __global__ __launch_bounds__(256) void mean_loss_kernel(const float* __restrict__ row_loss, int64_t rows,
                                                         float* __restrict__ out) {
@@ -256,7 +316,17 @@ int launch_softmax_xent(const float* logits, const float* labels, float* grad, f
                         int64_t rows, int64_t C, bool write_grad, hipStream_t s) {
   if (rows <= 0) return 0;
   const bool vec = C % 4 == 0 && ((uintptr_t)logits | (uintptr_t)labels | (uintptr_t)grad) % 16 == 0;
-  if (vec)
+  const int64_t nv4 = ceil_div(C / 4, 256);
+  if (vec && C >= 2048 && nv4 <= 8) {
+    const dim3 g((unsigned)rows);
+#define NSH_XENT(N_)                                                                                        \
+  hipLaunchKernelGGL(softmax_xent_row_kernel<N_>, g, dim3(256), 0, s, logits, labels, grad, row_loss, rows, C, \
+                     write_grad ? 1 : 0)
+    if (nv4 <= 2) NSH_XENT(2);
+    else if (nv4 <= 4) NSH_XENT(4);
+    else NSH_XENT(8);
+#undef NSH_XENT
+  } else if (vec)
     hipLaunchKernelGGL(softmax_xent_vec_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, logits, labels,
                        grad, row_loss, rows, C, write_grad ? 1 : 0);
   else
