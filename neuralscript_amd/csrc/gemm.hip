@@ -29,44 +29,43 @@ namespace nship {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int BM = 128, BN = 128, BK = 16;  // one 2x2-wave tile; the M side doubles with 4x2 waves
 constexpr int KPAD = 4;    // pitch of k-contiguous rows: 20 floats
-constexpr int RPAD = 4;    // pitch of row-contiguous k rows: 132 floats
+constexpr int RPAD = 4;    // pitch of row-contiguous k rows: ROWS + 4 floats
 constexpr int NT = 256;
 
-// LDS floats for one operand tile in either layout.
-constexpr int KC_TILE = BM * (BK + KPAD);   // [128][20]
-constexpr int MC_TILE = BK * (BM + RPAD);   // [16][132]
-
-template <bool KC>
+// LDS layout of one ROWS x 16 operand tile.
+template <bool KC, int ROWS>
 struct TileLayout;
-template <>
-struct TileLayout<true> {  // [rows][k], k contiguous
-  static constexpr int kSize = KC_TILE;
+template <int ROWS>
+struct TileLayout<true, ROWS> {  // [rows][k], k contiguous
+  static constexpr int kSize = ROWS * (BK + KPAD);
   __device__ static int at(int row, int k) { return row * (BK + KPAD) + k; }
 };
-template <>
-struct TileLayout<false> {  // [k][rows], rows contiguous
-  static constexpr int kSize = MC_TILE;
-  __device__ static int at(int row, int k) { return k * (BM + RPAD) + row; }
+template <int ROWS>
+struct TileLayout<false, ROWS> {  // [k][rows], rows contiguous
+  static constexpr int kSize = BK * (ROWS + RPAD);
+  __device__ static int at(int row, int k) { return k * (ROWS + RPAD) + row; }
 };
 
-// Global -> register staging of one 128x16 operand tile.
+// Global -> register staging of one ROWS x 16 operand tile by NTH threads.
 //  KC: element (row, k) at base[row*ld + k]   (k contiguous)
 //  MC: element (row, k) at base[k*ld + row]   (row contiguous)
 // `rows` = extent of the row dimension (M or N), `K` = contraction extent.
-template <bool KC, bool VEC>
+template <bool KC, bool VEC, int ROWS, int NTH>
 struct Stage {
-  float v[8];
+  static constexpr int kVec = ROWS * BK / 4 / NTH;  // float4 per thread (VEC)
+  static constexpr int kSca = ROWS * BK / NTH;      // floats per thread
+  float v[kSca];
   // rmap (optional): row r of the operand is row rmap[r] of `base`.
   __device__ void load(const float* __restrict__ base, int64_t ld, int row0, int rows, int k0, int K,
                        int t, const int* __restrict__ rmap = nullptr) {
     if (VEC) {
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int idx = t + NT * i;
+      for (int i = 0; i < kVec; i++) {
+        const int idx = t + NTH * i;
         int r, k;
-        if (KC) { r = idx >> 2; k = (idx & 3) * 4; } else { k = idx >> 5; r = (idx & 31) * 4; }
+        if (KC) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; } else { k = idx / (ROWS / 4); r = (idx % (ROWS / 4)) * 4; }
         const int gr = row0 + r, gk = k0 + k;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         // Whole float4 in or out: the contiguous extent is a multiple of 4.
@@ -79,10 +78,10 @@ struct Stage {
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int idx = t + NT * i;
+      for (int i = 0; i < kSca; i++) {
+        const int idx = t + NTH * i;
         int r, k;
-        if (KC) { r = idx >> 4; k = idx & 15; } else { k = idx >> 7; r = idx & 127; }
+        if (KC) { r = idx / BK; k = idx % BK; } else { k = idx / ROWS; r = idx % ROWS; }
         const int gr = row0 + r, gk = k0 + k;
         float x = 0.f;
         if (gr < rows && gk < K) {
@@ -96,34 +95,34 @@ struct Stage {
   __device__ void store(float* __restrict__ lds, int t) const {
     if (VEC) {
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int idx = t + NT * i;
+      for (int i = 0; i < kVec; i++) {
+        const int idx = t + NTH * i;
         int r, k;
-        if (KC) { r = idx >> 2; k = (idx & 3) * 4; } else { k = idx >> 5; r = (idx & 31) * 4; }
-        float* p = lds + TileLayout<KC>::at(r, k);
+        if (KC) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; } else { k = idx / (ROWS / 4); r = (idx % (ROWS / 4)) * 4; }
+        float* p = lds + TileLayout<KC, ROWS>::at(r, k);
         *reinterpret_cast<float4*>(p) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const int idx = t + NT * i;
+      for (int i = 0; i < kSca; i++) {
+        const int idx = t + NTH * i;
         int r, k;
-        if (KC) { r = idx >> 4; k = idx & 15; } else { k = idx >> 7; r = idx & 127; }
-        lds[TileLayout<KC>::at(r, k)] = v[i];
+        if (KC) { r = idx / BK; k = idx % BK; } else { k = idx / ROWS; r = idx % ROWS; }
+        lds[TileLayout<KC, ROWS>::at(r, k)] = v[i];
       }
     }
   }
 };
 
 // Four operand values of one lane for MFMA steps q = 0..3 of group g.
-template <bool KC>
+template <bool KC, int ROWS>
 __device__ __forceinline__ void read_frag(const float* __restrict__ lds, int row, int kb, float f[4]) {
   if (KC) {
-    const float4 x = *reinterpret_cast<const float4*>(lds + TileLayout<true>::at(row, kb));
+    const float4 x = *reinterpret_cast<const float4*>(lds + TileLayout<true, ROWS>::at(row, kb));
     f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
   } else {
 #pragma unroll
-    for (int q = 0; q < 4; q++) f[q] = lds[TileLayout<false>::at(row, kb + q)];
+    for (int q = 0; q < 4; q++) f[q] = lds[TileLayout<false, ROWS>::at(row, kb + q)];
   }
 }
 
@@ -149,8 +148,11 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
 // PLAIN: no row gather/scatter, no row scale, epilogue mode kEpiAct.
-template <bool TA, bool TB, bool VEC, bool PLAIN>
-__global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
+// WMW = 2: 4x2 waves (512 threads), workgroup tile 256 x 128: a quarter
+// fewer operand loads and LDS stores per FLOP (dense, non-grouped).
+template <bool TA, bool TB, bool VEC, bool PLAIN, int WMW>
+__global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(GemmArgs g) {
+  constexpr int BMT = BM * WMW, NTT = NT * WMW;
   const int M = g.M, N = g.N, K = g.K;
   const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
     C += (int64_t)blockIdx.z * g.sCk;
   }
   constexpr bool AKC = !TA, BKC = TB;
-  constexpr int ASZ = TileLayout<AKC>::kSize, BSZ = TileLayout<BKC>::kSize;
+  constexpr int ASZ = TileLayout<AKC, BMT>::kSize, BSZ = TileLayout<BKC, BN>::kSize;
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
   // buffer b: A tile at smem + b*(ASZ+BSZ), B tile right after it
 
@@ -192,14 +194,14 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
     const int L = xcd_linear(blockIdx.x, T);
     const int entry = L / tiles_n;
     const int e = g.tiles[2 * entry], mt = g.tiles[2 * entry + 1];
-    m0 = g.seg[e] + mt * BM;
+    m0 = g.seg[e] + mt * BMT;
     m_end = g.seg[e + 1];
     n0 = (L % tiles_n) * BN;
     B += (int64_t)e * g.sBg;
   } else {
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    m0 = tm * BM;
+    m0 = tm * BMT;
     n0 = tn * BN;
   }
 
@@ -211,8 +213,8 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; v++) acc[r][c][v] = 0.f;
 
-  Stage<AKC, VEC> sa;
-  Stage<BKC, VEC> sb;
+  Stage<AKC, VEC, BMT, NTT> sa;
+  Stage<BKC, VEC, BN, NTT> sb;
   const int nk = (kend - kbeg + BK - 1) / BK;
   sa.load(A, lda, m0, m_end, kbeg, kend, t, g.a_rows);
   sb.load(B, ldb, n0, N, kbeg, kend, t);
@@ -234,9 +236,9 @@ __global__ __launch_bounds__(NT, VEC ? 4 : 1) void gemm_f32_kernel(GemmArgs g) {
       const int kb = 8 * g + 4 * kh;
       float fa[2][4], fb[2][4];
 #pragma unroll
-      for (int r = 0; r < 2; r++) read_frag<AKC>(as, wm * 64 + r * 32 + l32, kb, fa[r]);
+      for (int r = 0; r < 2; r++) read_frag<AKC, BMT>(as, wm * 64 + r * 32 + l32, kb, fa[r]);
 #pragma unroll
-      for (int c = 0; c < 2; c++) read_frag<BKC>(bs, wn * 64 + c * 32 + l32, kb, fb[c]);
+      for (int c = 0; c < 2; c++) read_frag<BKC, BN>(bs, wn * 64 + c * 32 + l32, kb, fb[c]);
 #pragma unroll
       for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -318,19 +320,24 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
                   (!tB || !g.kseg);
   const bool vec = va && vb;
-  g.tiles_m = (int)ceil_div(g.M, BM);
+  const bool plain = !g.c_rows && !g.row_scale && g.mode == kEpiAct;
+  // 256-row tiles for large dense plain NN products (grouped, gathered,
+  // K-grouped and split launches keep 128 x 128)
+  const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kchunk && !g.a_rows && g.M >= 2048;
+  const int bm = wide ? 2 * BM : BM;
+  g.tiles_m = (int)ceil_div(g.M, bm);
   g.tiles_n = (int)ceil_div(g.N, BN);
   // grouped: an upper bound on tile entries, sum_e ceil(n_e / BM) <= M/BM + E
   const int entries = g.groups ? g.tiles_m + g.groups : g.tiles_m;
   const int zs = g.kchunk ? (int)ceil_div(g.K, g.kchunk) : 1;
   const dim3 grid(entries * g.tiles_n, batch, zs), block(NT);
-  const bool plain = !g.c_rows && !g.row_scale && g.mode == kEpiAct;
-#define NSH_GEMM(TA_, TB_, V_)                                                                  \
-  do {                                                                                         \
-    if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true>), grid, block, 0, s, g);  \
-    else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false>), grid, block, 0, s, g);       \
+#define NSH_GEMM(TA_, TB_, V_)                                                                     \
+  do {                                                                                            \
+    if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true, 1>), grid, block, 0, s, g);  \
+    else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false, 1>), grid, block, 0, s, g);       \
   } while (0)
-  if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
+  if (wide) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 2>), grid, dim3(2 * NT), 0, s, g);
+  else if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
   else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
   else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
   else { if (vec) NSH_GEMM(true, true, true); else NSH_GEMM(true, true, false); }
