@@ -148,11 +148,11 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
 // PLAIN: no row gather/scatter, no row scale, epilogue mode kEpiAct.
-// WMW = 2: 4x2 waves (512 threads), workgroup tile 256 x 128: a quarter
-// fewer operand loads and LDS stores per FLOP (dense, non-grouped).
-template <bool TA, bool TB, bool VEC, bool PLAIN, int WMW>
-__global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(GemmArgs g) {
-  constexpr int BMT = BM * WMW, NTT = NT * WMW;
+// WMW = 2 / WNW = 2: 4x2 / 2x4 waves (512 threads), workgroup tile
+// 256 x 128 / 128 x 256: a quarter fewer operand loads and LDS stores per FLOP.
+template <bool TA, bool TB, bool VEC, bool PLAIN, int WMW, int WNW>
+__global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gemm_f32_kernel(GemmArgs g) {
+  constexpr int BMT = BM * WMW, BNT = BN * WNW, NTT = NT * WMW * WNW;
   const int M = g.M, N = g.N, K = g.K;
   const int64_t lda = g.lda, ldb = g.ldb, ldc = g.ldc;
   const int tiles_m = g.tiles_m, tiles_n = g.tiles_n;
@@ -172,13 +172,13 @@ __global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(G
     C += (int64_t)blockIdx.z * g.sCk;
   }
   constexpr bool AKC = !TA, BKC = TB;
-  constexpr int ASZ = TileLayout<AKC, BMT>::kSize, BSZ = TileLayout<BKC, BN>::kSize;
+  constexpr int ASZ = TileLayout<AKC, BMT>::kSize, BSZ = TileLayout<BKC, BNT>::kSize;
   __shared__ __attribute__((aligned(16))) float smem[2 * (ASZ + BSZ)];
   // buffer b: A tile at smem + b*(ASZ+BSZ), B tile right after it
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (2 * WNW), wn = wave % (2 * WNW);
   const int l32 = lane & 31, kh = lane >> 5;
 
   int m0, n0;
@@ -196,13 +196,13 @@ __global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(G
     const int e = g.tiles[2 * entry], mt = g.tiles[2 * entry + 1];
     m0 = g.seg[e] + mt * BMT;
     m_end = g.seg[e + 1];
-    n0 = (L % tiles_n) * BN;
+    n0 = (L % tiles_n) * BNT;
     B += (int64_t)e * g.sBg;
   } else {
     int tm, tn;
     tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     m0 = tm * BMT;
-    n0 = tn * BN;
+    n0 = tn * BNT;
   }
 
   floatx16 acc[2][2];
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(G
       for (int v = 0; v < 16; v++) acc[r][c][v] = 0.f;
 
   Stage<AKC, VEC, BMT, NTT> sa;
-  Stage<BKC, VEC, BN, NTT> sb;
+  Stage<BKC, VEC, BNT, NTT> sb;
   const int nk = (kend - kbeg + BK - 1) / BK;
   sa.load(A, lda, m0, m_end, kbeg, kend, t, g.a_rows);
   sb.load(B, ldb, n0, N, kbeg, kend, t);
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(NT * WMW, VEC ? 4 / WMW : 1) void gemm_f32_kernel(G
 #pragma unroll
       for (int r = 0; r < 2; r++) read_frag<AKC, BMT>(as, wm * 64 + r * 32 + l32, kb, fa[r]);
 #pragma unroll
-      for (int c = 0; c < 2; c++) read_frag<BKC, BN>(bs, wn * 64 + c * 32 + l32, kb, fb[c]);
+      for (int c = 0; c < 2; c++) read_frag<BKC, BNT>(bs, wn * 64 + c * 32 + l32, kb, fb[c]);
 #pragma unroll
       for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -321,22 +321,25 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
                   (!tB || !g.kseg);
   const bool vec = va && vb;
   const bool plain = !g.c_rows && !g.row_scale && g.mode == kEpiAct;
-  // 256-row tiles for large dense plain NN products (grouped, gathered,
-  // K-grouped and split launches keep 128 x 128)
+  // 256-row tiles for large dense plain NN products; 256-column tiles for
+  // the grouped (per-expert) NN products, whose row ranges are short
   const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kchunk && !g.a_rows && g.M >= 2048;
-  const int bm = wide ? 2 * BM : BM;
+  const bool tallg = !tA && !tB && vec && g.groups && !g.kseg && !g.kchunk && g.N >= 1024;
+  const int bm = wide ? 2 * BM : BM, bn = tallg ? 2 * BN : BN;
   g.tiles_m = (int)ceil_div(g.M, bm);
-  g.tiles_n = (int)ceil_div(g.N, BN);
+  g.tiles_n = (int)ceil_div(g.N, bn);
   // grouped: an upper bound on tile entries, sum_e ceil(n_e / BM) <= M/BM + E
   const int entries = g.groups ? g.tiles_m + g.groups : g.tiles_m;
   const int zs = g.kchunk ? (int)ceil_div(g.K, g.kchunk) : 1;
   const dim3 grid(entries * g.tiles_n, batch, zs), block(NT);
-#define NSH_GEMM(TA_, TB_, V_)                                                                     \
-  do {                                                                                            \
-    if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true, 1>), grid, block, 0, s, g);  \
-    else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false, 1>), grid, block, 0, s, g);       \
+#define NSH_GEMM(TA_, TB_, V_)                                                                        \
+  do {                                                                                               \
+    if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true, 1, 1>), grid, block, 0, s, g);  \
+    else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false, 1, 1>), grid, block, 0, s, g);       \
   } while (0)
-  if (wide) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 2>), grid, dim3(2 * NT), 0, s, g);
+  if (wide) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 2, 1>), grid, dim3(2 * NT), 0, s, g);
+  else if (tallg && plain) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 1, 2>), grid, dim3(2 * NT), 0, s, g);
+  else if (tallg) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, false, 1, 2>), grid, dim3(2 * NT), 0, s, g);
   else if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
   else if (!tA && tB) { if (vec) NSH_GEMM(false, true, true); else NSH_GEMM(false, true, false); }
   else if (tA && !tB) { if (vec) NSH_GEMM(true, false, true); else NSH_GEMM(true, false, false); }
