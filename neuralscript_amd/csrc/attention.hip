@@ -32,7 +32,8 @@ __device__ __forceinline__ float4 keep4(bool keep, float4 x) {
   return make_float4(keep ? x.x : 0.f, keep ? x.y : 0.f, keep ? x.z : 0.f, keep ? x.w : 0.f);
 }
 
-constexpr int kBQ = 128;  // queries per workgroup
+constexpr int kBQ = 128;  // queries (keys) per workgroup of the backward kernels
+constexpr int kFW = 8;     // forward: waves per workgroup (32 queries each), sharing every K/V tile
 constexpr int kBK = 64;   // keys per tile
 
 // Same bijective XCD-contiguous remap as the GEMM.
@@ -80,15 +81,15 @@ struct KVTile {
 
 // One K or V tile (64 keys x DK) in registers on its way to LDS (row pitch
 // DK + 4); rows past the end load a clamped row and are zeroed.
-template <int DK>
+template <int DK, int NTH>
 struct HalfTile {
   static constexpr int P = DK + 4;
-  static constexpr int kPer = kBK * DK / 4 / 256;
+  static constexpr int kPer = kBK * DK / 4 / NTH;
   float4 r[kPer];
   __device__ void load(const float* __restrict__ X, int64_t ld, int hcol, int key0, int S, int t) {
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
-      const int idx = t + 256 * i;
+      const int idx = t + NTH * i;
       const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
       const int gk = key0 + key;
       const bool in = gk < S;
@@ -99,7 +100,7 @@ struct HalfTile {
   __device__ void store(float* __restrict__ xs, int t) const {
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
-      const int idx = t + 256 * i;
+      const int idx = t + NTH * i;
       *reinterpret_cast<float4*>(xs + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = r[i];
     }
   }
@@ -134,7 +135,7 @@ __device__ __forceinline__ void score_tile(const float* __restrict__ ks, const f
 // exp2(m_old - m_new) is skipped when no lane's running max moved (the factor
 // would be exactly 1).
 template <int DK>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+__global__ __launch_bounds__(kFW * 64) void flash_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                         const float* __restrict__ V, float* __restrict__ ctx,
                                                         float* __restrict__ lse, int S, int H, int64_t ld,
                                                         float scale_log2, int nqb) {
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
   const int L = remap_xcd(blockIdx.x, nqb * H);
-  const int h = L / nqb, q0 = (L % nqb) * kBQ;
+  const int h = L / nqb, q0 = (L % nqb) * (32 * kFW);
   const int hcol = h * DK;
   const int qrow = q0 + w * 32 + l32;
 
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
   float m = -INFINITY, l = 0.f;
 
   const int nkv = (S + kBK - 1) / kBK;
-  HalfTile<DK> tk, tv;
+  HalfTile<DK, kFW * 64> tk, tv;
   tk.load(K, ld, hcol, 0, S, t);
   tv.load(V, ld, hcol, 0, S, t);
   tk.store(kbuf, t);
@@ -252,6 +253,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(const float* __restrict_
   if (lse && kh == 0 && qrow < S) lse[(int64_t)h * S + qrow] = m + log2f(l);
 
   // O^T (d, query) / l  ->  LDS [query][d]  ->  coalesced rows of ctx.
+  static_assert(kFW * 32 * (DK + 1) <= 4 * TF, "output staging fits the K/V buffers");
   const float inv = 1.f / l;
   float* T = sm + w * 32 * (DK + 1);
 #pragma unroll
@@ -787,8 +789,8 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
   const float scale = 1.0f / sqrtf((float)DK);
   const bool aligned = ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) % 16 == 0;
   if (aligned && (DK == 64 || DK == 32)) {
-    const int nqb = (int)ceil_div(S, kBQ);
-    const dim3 grid(nqb * (unsigned)H), block(256);
+    const int nqb = (int)ceil_div(S, 32 * kFW);
+    const dim3 grid(nqb * (unsigned)H), block(64 * kFW);
     const float sl2 = scale * 1.4426950408889634f;
     if (DK == 64)
       hipLaunchKernelGGL(flash_fwd_kernel<64>, grid, block, 0, s, Q, K, V, ctx, lse, (int)S, (int)H, ld, sl2, nqb);
