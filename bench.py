@@ -324,8 +324,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
-        raise SystemExit("bench.py: this build measures one GPU only (single-GPU boxes; "
-                         "see DESIGN.md for how the path would shard)")
+        raise SystemExit("bench.py: this build measures one GPU only (the path runs on one GPU; "
+                         "--gpus must be 1)")
     if a.config == "copy":
         res = copy_calibration()
     elif a.config == "c2":
