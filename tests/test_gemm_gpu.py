@@ -9,8 +9,10 @@ from neuralscript_amd import runtime, synth
 
 pytestmark = pytest.mark.gpu
 
+# M >= 2048 (nn) runs the 256-row tiles: (2050, 260, 100) has ragged edges on every side
 SHAPES = [(1, 1, 1), (3, 5, 2), (37, 45, 29), (128, 128, 16), (130, 257, 100),
-          (256, 384, 64), (513, 129, 1031), (1024, 1024, 1024), (8, 4096, 512)]
+          (256, 384, 64), (513, 129, 1031), (1024, 1024, 1024), (8, 4096, 512), (2050, 260, 100),
+          (4096, 384, 256)]
 
 
 def operands(M, N, K, seed):
@@ -41,9 +43,9 @@ def test_gemm_matches_oracle(M, N, K, variant):
     helpers.assert_close(gC.to_host(), ref, f"gemm {variant} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(70, 96, 48), (2100, 136, 32)])
 @pytest.mark.parametrize("act", range(7))
-def test_gemm_fused_activation_epilogue(act):
-    M, N, K = 70, 96, 48
+def test_gemm_fused_activation_epilogue(act, M, N, K):
     A, B = operands(M, N, K, 500 + act)
     ref = oracle.matmul(A, B, M, K, N, act)
     gA, gB = runtime.DeviceArray.from_host(A), runtime.DeviceArray.from_host(B)
