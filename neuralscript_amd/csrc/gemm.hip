@@ -147,7 +147,8 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
-// PLAIN: no row gather/scatter, no row scale, epilogue mode kEpiAct.
+// PLAIN: no row gather/scatter, no row scale; epilogue kEpiAct (with the
+// pre-activation / activation pair when C2 is set) or kEpiAccum.
 // WMW = 2 / WNW = 2: 4x2 / 2x4 waves (512 threads), workgroup tile
 // 256 x 128 / 128 x 256: a quarter fewer operand loads and LDS stores per FLOP.
 template <bool TA, bool TB, bool VEC, bool PLAIN, int WMW, int WNW>
@@ -265,13 +266,30 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
       for (int c = 0; c < 2; c++) {
         const int col = n0 + wn * 64 + c * 32 + l32;
         const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
-        float* __restrict__ cp = C + (int64_t)row0 * ldc + col;
+        float* cp = C + (int64_t)row0 * ldc + col;
         const bool cin = col < N;
 #define NSH_STORE16(CODE)                                                          \
   _Pragma("unroll") for (int v = 0; v < 16; v++) {                                 \
     const int dr = 8 * (v >> 2) + (v & 3);                                         \
     if (cin && row0 + dr < m_end) cp[(int64_t)dr * ldc] = act_apply(acc[r][c][v], CODE); \
   }
+        if (g.mode == kEpiAccum) {
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int dr = 8 * (v >> 2) + (v & 3);
+            if (cin && row0 + dr < m_end) cp[(int64_t)dr * ldc] += acc[r][c][v];
+          }
+          continue;
+        }
+        if (g.C2) {
+          // pre-activation to C, then the activation to C2 below
+#pragma unroll
+          for (int v = 0; v < 16; v++) {
+            const int dr = 8 * (v >> 2) + (v & 3);
+            if (cin && row0 + dr < m_end) cp[(int64_t)dr * ldc] = acc[r][c][v];
+          }
+          cp = g.C2 + (int64_t)blockIdx.y * g.sC + (int64_t)row0 * ldc + col;
+        }
         switch (g.act) {
           case kActRelu: NSH_STORE16(kActRelu); break;
           case kActLeaky: NSH_STORE16(kActLeaky); break;
@@ -320,7 +338,9 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
                   (!tB || !g.kseg);
   const bool vec = va && vb;
-  const bool plain = !g.c_rows && !g.row_scale && g.mode == kEpiAct;
+  // plain epilogue: no row maps or scaling; activation, accumulate or the
+  // pre-activation / activation pair (kchunk partials are always kEpiAct)
+  const bool plain = !g.c_rows && !g.row_scale && (g.mode == kEpiAct || g.mode == kEpiAccum);
   // 256-row tiles for large dense plain NN products; 256-column tiles for
   // the grouped (per-expert) NN products, whose row ranges are short
   const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kchunk && !g.a_rows && g.M >= 2048;
@@ -368,7 +388,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 static bool splittable(const GemmArgs& g) {
-  return !g.groups && !g.kseg && !g.a_rows && !g.c_rows && !g.row_scale && g.kchunk == 0;
+  return !g.groups && !g.kseg && !g.a_rows && !g.c_rows && !g.row_scale && !g.C2 && g.kchunk == 0;
 }
 
 // Chunk length for `splits` chunks: a multiple of BK (and so of 4, keeping

@@ -25,6 +25,9 @@ struct GemmArgs {
   int mode = kEpiAct;
   const float* aux = nullptr;
   int64_t ldaux = 0;
+  // kEpiAct with C2 set: C = acc and C2 = act(acc), same pitch (a training
+  // forward keeps the pre-activation for the backward pass)
+  float* C2 = nullptr;
   // Row gather / scatter (!transA only): operand-A row r is A row a_rows[r];
   // output row r goes to C row c_rows[r], scaled by row_scale[c_rows[r]].
   const int* a_rows = nullptr;

@@ -10,6 +10,7 @@
 // batch; the host blob copy is refreshed lazily after training.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -722,7 +723,33 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
     const Instr& I = F.ins[ii];
     if (skip[ii] || I.op == Op::Marker) continue;
     switch (I.op) {
-      case Op::Matmul: case Op::Act: case Op::Embedding: case Op::LayerNorm: case Op::Attention: case Op::Moe:
+      case Op::Matmul: {
+        // MATMUL then ACTIVATION of its result: one GEMM writes both the
+        // pre-activation (kept for the backward pass) and the activation
+        const Instr* J = ii + 1 < F.ins.size() ? &F.ins[ii + 1] : nullptr;
+        if (J && J->op == Op::Act && J->in[0] == I.res && I.act == 0 && !I.in_group) {
+          const int64_t K = I.k, N = I.n;
+          const int64_t M = (int64_t)(fr.numel[I.in[0]] / (size_t)K);
+          if (fr.numel[I.in[1]] < (size_t)(K * N) || M > INT32_MAX) {
+            set_error("matmul: operand '" + P.vals[I.in[1]].name + "' is smaller than its static shape");
+            return -1;
+          }
+          NSH_OUT(C, I.res, (size_t)(M * N));
+          NSH_OUT(Y, J->res, (size_t)(M * N));
+          GemmArgs g;
+          g.A = fr.ptr[I.in[0]]; g.B = fr.ptr[I.in[1]]; g.C = C; g.C2 = Y;
+          g.M = (int)M; g.N = (int)N; g.K = (int)K;
+          g.lda = K; g.ldb = N; g.ldc = N;
+          g.act = J->act;
+          Prof p(m, "gemm");
+          if (rt_gemm_ex(m, g, false, false, 1) != 0) return -1;
+          skip[ii + 1] = true;
+          break;
+        }
+        if (exec_forward_op(m, F, I, fr, true) != 0) return -1;
+        break;
+      }
+      case Op::Act: case Op::Embedding: case Op::LayerNorm: case Op::Attention: case Op::Moe:
       case Op::Dropout: case Op::Softmax:
         if (exec_forward_op(m, F, I, fr, true) != 0) return -1;
         break;
@@ -779,16 +806,20 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             g.M = (int)M; g.N = (int)K; g.K = (int)N;
             g.lda = N; g.ldb = N; g.ldc = K;
             int res = I.res;
-            if (ii + 1 < F.ins.size()) {
-              const Instr& J = F.ins[ii + 1];
-              if (J.op == Op::ActGrad && !J.dropout && J.in[0] == I.res && uses_of(F, I.res) == 1) {
+            // the ACTIVATION_GRAD of this result (its only use; a
+            // MATMUL_GRAD_W may come first) runs in the GEMM's epilogue
+            for (size_t jj = ii + 1; jj < F.ins.size() && uses_of(F, I.res) == 1; jj++) {
+              const Instr& J = F.ins[jj];
+              if (std::find(J.in.begin(), J.in.end(), I.res) == J.in.end()) continue;
+              if (J.op == Op::ActGrad && !J.dropout && J.in[0] == I.res && fr.ptr[J.in[1]]) {
                 g.mode = kEpiActGrad;
                 g.act = J.act;
                 g.aux = fr.ptr[J.in[1]];
                 g.ldaux = K;
                 res = J.res;
-                skip[ii + 1] = true;
+                skip[jj] = true;
               }
+              break;
             }
             NSH_OUT(C, res, (size_t)(M * K));
             g.C = C;
