@@ -142,9 +142,21 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     model = runtime.Model(runtime.Plan(ir), w)
     model.train_step(x, y, 0.02)
     bad = []
+    # a MATMUL_GRAD_A result whose only use is an ACTIVATION_GRAD is folded
+    # into that GEMM's epilogue and never stored; the activation gradient
+    # computed from it is checked instead
+    uses = {}
+    for ins in net.train.instrs:
+        for o in ins.operands:
+            uses[o] = uses.get(o, 0) + 1
+    folded = {i.operands[0] for i in net.train.instrs
+              if i.op == "ns.grad.activation" and "dropout_mask" not in i.comment and uses.get(i.operands[0]) == 1}
     for ins in net.train.instrs:
         v = ins.result
         if v is None or v not in rec["buf"] or ins.op in ("ns.cross_entropy",):
+            continue
+        if ins.op == "ns.grad.matmul.a" and v in folded:
+            print(f"  {ins.op:24s} {v:8s} folded into its activation gradient's GEMM epilogue")
             continue
         ref = rec["buf"][v]
         got = model.read_value(v, ref.size)
@@ -194,3 +206,4 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
         assert d <= 2e-3, n_
     assert not bad, bad
     model.free()
+
