@@ -188,6 +188,42 @@ def c5_work(M=16384, D=512, H=8, V=8192, FF=2048, C=8192):
             "total": 3 * dense_fwd + 12.0 * M * M * D}
 
 
+def c5_hbm_bytes(n_muon, M=16384, D=512, C=8192):
+    """Algorithmic HBM bytes per step of c5's bandwidth-bound regions: CE reads
+    the logits and the one-hot labels and writes the gradient ([M, C] each);
+    the Muon gather reads g and writes its transpose, the update reads the q
+    vectors and w and writes w (n_muon elements each); embedding and LayerNorm
+    read and write [M, D] (LayerNorm's gradient also reads x)."""
+    return {"softmax_xent": 3.0 * M * C * 4, "muon_gather": 2.0 * n_muon * 4, "muon_update": 3.0 * n_muon * 4,
+            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4}
+
+
+def adamw_bandwidth(n, launches=20):
+    """The AdamW kernel (nsh_op_adamw_step) over n parameters, as if every
+    weight of the step took AdamW: 4 arrays read, 3 written (28 bytes per
+    parameter), timed over `launches` back-to-back launches."""
+    import ctypes
+    from neuralscript_amd import runtime
+    bufs = [runtime.DeviceArray(n) for _ in range(4)]
+    for b in bufs:
+        b.fill_zero()
+    w, g, m, v = (b.ptr for b in bufs)
+    lib = runtime.lib()
+    lr = ctypes.c_float(3e-4)
+    lib.nsh_op_adamw_step(w, g, m, v, n, 1, lr)
+    runtime.check(lib.nsh_device_synchronize(), "synchronize")
+    t0 = time.perf_counter()
+    for t in range(launches):
+        lib.nsh_op_adamw_step(w, g, m, v, n, t + 2, lr)
+    runtime.check(lib.nsh_device_synchronize(), "synchronize")
+    us = (time.perf_counter() - t0) / launches * 1e6
+    for b in bufs:
+        b.free()
+    gbs = 28.0 * n / (us * 1e-6) / 1e9
+    return {"params": n, "us_per_launch": us, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+            "note": "the whole parameter count of the step through the AdamW kernel (28 B per parameter)"}
+
+
 def bench_train(key, steps, warmup):
     """Device-resident training steps of config `key` (nsh_train_step_device);
     lr = 3e-4 times the cosine-warmup multiplier, as the host applies it."""
@@ -218,7 +254,18 @@ def bench_train(key, steps, warmup):
     loss = model.train_step_device(dx, dy, 3e-4 * scale(t))
     model.free()
     work = c5_work()
-    kernels = {k: {"ms_per_step": v["ms"] / steps, "calls_per_step": v["calls"] / steps} for k, v in prof.items()}
+    shapes = workloads.ir_shapes(plan.ir)
+    # Muon matrices (codegen.cpp:3097): every 2-D weight with min(r, c) >= 8
+    n_muon = sum(int(np.prod(v)) for v in shapes.values() if len(v) == 2 and min(v) >= 8)
+    hbm = c5_hbm_bytes(n_muon)
+    kernels = {}
+    for k, v in prof.items():
+        ms = v["ms"] / steps
+        e = {"ms_per_step": ms, "calls_per_step": v["calls"] / steps}
+        if k in hbm:
+            e["GB/s"] = hbm[k] / (ms * 1e-3) / 1e9
+            e["hbm_frac"] = e["GB/s"] / HBM_PEAK_GBS
+        kernels[k] = e
     att = prof["attention_bwd"]
     return {"metric": METRIC, "value": steps / dt, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
             "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -226,7 +273,7 @@ def bench_train(key, steps, warmup):
             "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device"},
             "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
             "roofline": roofline_of(key, "attention_bwd", work["attention_bwd"], att["ms"] / att["calls"]),
-            "kernels": kernels}
+            "kernels": kernels, "adamw": adamw_bandwidth(n_muon)}
 
 
 def bench_c2(steps, warmup, with_cpu):

@@ -39,20 +39,44 @@ constexpr int kPanelThreads = 1024;
 constexpr int kPanelWaves = kPanelThreads / 64;
 constexpr int kMaxPanelR = 8 * kPanelThreads;
 
+// One AdamW element (codegen.cpp:1617-1633), contraction off so every
+// product and sum rounds as the reference's scalar code does.
+__device__ __forceinline__ void adamw_elem(float& w, float gg, float& m, float& v, float lr, float b1t, float b2t) {
+#pragma clang fp contract(off)
+  const float mi = 0.9f * m + 0.1f * gg;
+  const float vi = 0.999f * v + 0.001f * gg * gg;
+  m = mi;
+  v = vi;
+  const float mh = mi / b1t, vh = vi / b2t;
+  w = w - ((lr * mh / (sqrtf(vh) + 1e-8f)) + (0.01f * lr) * w);
+}
+
+// VEC: thread i updates elements 4i..4i+3 with float4 loads and stores (all
+// four arrays 16-byte aligned; the n % 4 tail goes to the first threads);
+// else one element per thread.
+template <bool VEC>
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ w, const float* __restrict__ g,
                                                     float* __restrict__ m, float* __restrict__ v, int64_t n, float lr,
                                                     float b1t, float b2t) {
-#pragma clang fp contract(off)
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float gg = g[i];
-  const float mi = 0.9f * m[i] + 0.1f * gg;
-  const float vi = 0.999f * v[i] + 0.001f * gg * gg;
-  m[i] = mi;
-  v[i] = vi;
-  const float mh = mi / b1t, vh = vi / b2t;
-  const float wi = w[i];
-  w[i] = wi - ((lr * mh / (sqrtf(vh) + 1e-8f)) + (0.01f * lr) * wi);
+  if constexpr (VEC) {
+    const int64_t n4 = n / 4;
+    if (i < n4) {
+      const fvec4 w4 = ((gfloat4*)as_global(w))[i], m4 = ((gfloat4*)as_global(m))[i];
+      const fvec4 v4 = ((gfloat4*)as_global(v))[i], g4 = ((const gfloat4*)as_global(g))[i];
+      float W[4] = {w4.x, w4.y, w4.z, w4.w}, Mo[4] = {m4.x, m4.y, m4.z, m4.w}, Vo[4] = {v4.x, v4.y, v4.z, v4.w};
+      const float G[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) adamw_elem(W[e], G[e], Mo[e], Vo[e], lr, b1t, b2t);
+      ((gfloat4*)as_global(m))[i] = fvec4{Mo[0], Mo[1], Mo[2], Mo[3]};
+      ((gfloat4*)as_global(v))[i] = fvec4{Vo[0], Vo[1], Vo[2], Vo[3]};
+      ((gfloat4*)as_global(w))[i] = fvec4{W[0], W[1], W[2], W[3]};
+    }
+    const int64_t t = 4 * n4 + i;
+    if (i < 4 && t < n) adamw_elem(w[t], g[t], m[t], v[t], lr, b1t, b2t);
+  } else {
+    if (i < n) adamw_elem(w[i], g[i], m[i], v[i], lr, b1t, b2t);
+  }
 }
 
 // Block-wide sum (256 threads), fixed tree.
@@ -65,17 +89,64 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// float4 access needs R and C multiples of 4 and 16-byte aligned bases (the
+// blob's matrices start anywhere a float can).
+__device__ __forceinline__ bool vec4_ok(int64_t R, int64_t C, const void* a, const void* b) {
+  return ((R | C) & 3) == 0 && (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
+}
+
 // T = the vectors of g, contiguous: r < c, the rows (a copy); r >= c, the
-// columns, T[j][k] = g[k][j], transposed in 32 x 32 tiles through LDS so both
-// sides are read and written along rows.  grid.y = matrix.
+// columns, T[j][k] = g[k][j], transposed through LDS so both sides are read
+// and written along rows: 64 x 64 tiles with float4 on both sides (the LDS
+// row pitch of 65 keeps the column reads conflict-free), or 32 x 32 scalar
+// tiles where float4 does not fit.  grid.y = matrix.
 __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restrict__ mats, int nmat) {
-  __shared__ float tile[32][33];
+  __shared__ float tile[64 * 65];
   const MuonMat& M = mats[blockIdx.y];
   const gfloat* __restrict__ g = as_global(M.g);
   gfloat* __restrict__ T = as_global(M.T);
   const int64_t R = M.R, C = M.C;
+  const bool vec = vec4_ok(R, C, M.g, M.T);
   if (M.transposed) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256) T[i] = g[i];
+    if (vec) {
+      const gfloat4* g4 = (const gfloat4*)g;
+      gfloat4* T4 = (gfloat4*)T;
+      for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C / 4; i += (int64_t)gridDim.x * 256)
+        T4[i] = g4[i];
+    } else {
+      for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256)
+        T[i] = g[i];
+    }
+    return;
+  }
+  if (vec) {
+    // thread: float4 column q (of 16 per 64-wide row), rows rr + 16 i
+    const int q = threadIdx.x & 15, rr = threadIdx.x >> 4;
+    const int64_t tc = (C + 63) / 64, tiles = ((R + 63) / 64) * tc;
+    for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
+      const int64_t k0 = (b / tc) * 64, j0 = (b % tc) * 64;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = rr + 16 * i;
+        if (k0 + r < R && j0 + 4 * q < C) {
+          const fvec4 x = *(const gfloat4*)(g + (k0 + r) * C + j0 + 4 * q);
+          float* t = tile + r * 65 + 4 * q;
+          t[0] = x.x, t[1] = x.y, t[2] = x.z, t[3] = x.w;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int jj = rr + 16 * i;
+        if (j0 + jj < C && k0 + 4 * q < R) {
+          const float* t = tile + 4 * q * 65 + jj;
+          fvec4 y;
+          y.x = t[0], y.y = t[65], y.z = t[130], y.w = t[195];
+          *(gfloat4*)(T + (j0 + jj) * R + k0 + 4 * q) = y;
+        }
+      }
+      __syncthreads();
+    }
     return;
   }
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
@@ -83,10 +154,10 @@ __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restr
   for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
     const int64_t k0 = (b / tc) * 32, j0 = (b % tc) * 32;
     for (int r = ty; r < 32; r += 8)
-      if (k0 + r < R && j0 + tx < C) tile[r][tx] = g[(k0 + r) * C + j0 + tx];
+      if (k0 + r < R && j0 + tx < C) tile[r * 33 + tx] = g[(k0 + r) * C + j0 + tx];
     __syncthreads();
     for (int r = ty; r < 32; r += 8)
-      if (j0 + r < C && k0 + tx < R) T[(j0 + r) * R + k0 + tx] = tile[tx][r];
+      if (j0 + r < C && k0 + tx < R) T[(j0 + r) * R + k0 + tx] = tile[tx * 33 + r];
     __syncthreads();
   }
   (void)nmat;
@@ -339,19 +410,69 @@ __global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat*
 }
 
 // w -= le * q + (0.01 lr) * w, q = T (normalised vectors): element [k][j]
-// of w takes q_j[k] (r >= c, through 32 x 32 LDS tiles) or q_k[j] (r < c).
+// of w takes q_j[k] (r >= c, through LDS tiles laid out as in the gather) or
+// q_k[j] (r < c).
 __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restrict__ mats, int nmat) {
 #pragma clang fp contract(off)
-  __shared__ float tile[32][33];
+  __shared__ float tile[64 * 65];
   const MuonMat& M = mats[blockIdx.y];
   const gfloat* __restrict__ T = as_global(M.T);
   gfloat* __restrict__ w = as_global(M.w);
   const int64_t R = M.R, C = M.C;
   const float le = M.le, decay = M.decay;
+  const bool vec = vec4_ok(R, C, M.w, M.T);
   if (M.transposed) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256) {
-      const float wi = w[i];
-      w[i] = wi - (le * T[i] + decay * wi);
+    if (vec) {
+      const gfloat4* T4 = (const gfloat4*)T;
+      gfloat4* w4 = (gfloat4*)w;
+      for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C / 4; i += (int64_t)gridDim.x * 256) {
+        const fvec4 wi = w4[i], ti = T4[i];
+        fvec4 o;
+        o.x = wi.x - (le * ti.x + decay * wi.x);
+        o.y = wi.y - (le * ti.y + decay * wi.y);
+        o.z = wi.z - (le * ti.z + decay * wi.z);
+        o.w = wi.w - (le * ti.w + decay * wi.w);
+        w4[i] = o;
+      }
+    } else {
+      for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < R * C; i += (int64_t)gridDim.x * 256) {
+        const float wi = w[i];
+        w[i] = wi - (le * T[i] + decay * wi);
+      }
+    }
+    return;
+  }
+  if (vec) {
+    const int q = threadIdx.x & 15, rr = threadIdx.x >> 4;
+    const int64_t tr = (R + 63) / 64, tiles = tr * ((C + 63) / 64);
+    for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
+      const int64_t j0 = (b / tr) * 64, k0 = (b % tr) * 64;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int jj = rr + 16 * i;
+        if (j0 + jj < C && k0 + 4 * q < R) {
+          const fvec4 x = *(const gfloat4*)(T + (j0 + jj) * R + k0 + 4 * q);
+          float* t = tile + jj * 65 + 4 * q;
+          t[0] = x.x, t[1] = x.y, t[2] = x.z, t[3] = x.w;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = rr + 16 * i;
+        if (k0 + r < R && j0 + 4 * q < C) {
+          const float* t = tile + 4 * q * 65 + r;
+          gfloat4* wp = (gfloat4*)(w + (k0 + r) * C + j0 + 4 * q);
+          const fvec4 wi = *wp;
+          fvec4 o;
+          o.x = wi.x - (le * t[0] + decay * wi.x);
+          o.y = wi.y - (le * t[65] + decay * wi.y);
+          o.z = wi.z - (le * t[130] + decay * wi.z);
+          o.w = wi.w - (le * t[195] + decay * wi.w);
+          *wp = o;
+        }
+      }
+      __syncthreads();
     }
     return;
   }
@@ -360,13 +481,13 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restr
   for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
     const int64_t j0 = (b / tr) * 32, k0 = (b % tr) * 32;
     for (int r = ty; r < 32; r += 8)
-      if (j0 + r < C && k0 + tx < R) tile[r][tx] = T[(j0 + r) * R + k0 + tx];
+      if (j0 + r < C && k0 + tx < R) tile[r * 33 + tx] = T[(j0 + r) * R + k0 + tx];
     __syncthreads();
     for (int r = ty; r < 32; r += 8)
       if (k0 + r < R && j0 + tx < C) {
         const int64_t i = (k0 + r) * C + j0 + tx;
         const float wi = w[i];
-        w[i] = wi - (le * tile[tx][r] + decay * wi);
+        w[i] = wi - (le * tile[tx * 33 + r] + decay * wi);
       }
     __syncthreads();
   }
@@ -378,7 +499,12 @@ __global__ __launch_bounds__(256) void muon_update_kernel(const MuonMat* __restr
 int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1t, float b2t,
                  hipStream_t s) {
   if (n <= 0) return 0;
-  hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, w, g, m, v, n, lr, b1t, b2t);
+  if ((((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) & 15) == 0 && n >= 4)
+    hipLaunchKernelGGL(adamw_kernel<true>, dim3((unsigned)ceil_div(n / 4, 256)), dim3(256), 0, s, w, g, m, v, n, lr,
+                       b1t, b2t);
+  else
+    hipLaunchKernelGGL(adamw_kernel<false>, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, w, g, m, v, n, lr,
+                       b1t, b2t);
   NSH_LAUNCHED();
   return 0;
 }
@@ -387,7 +513,8 @@ int muon_blocks(int C) { return (int)ceil_div(C, kCPB) > 0 ? (int)ceil_div(C, kC
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
-  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 1024), 4096);
+  // one workgroup per 64 x 64 tile of the largest matrix
+  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 4096), 4096);
   hipLaunchKernelGGL(muon_gather_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
   NSH_LAUNCHED();
   return 0;
@@ -427,7 +554,8 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
 
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
-  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 1024), 4096);
+  // one workgroup per 64 x 64 tile of the largest matrix
+  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 4096), 4096);
   hipLaunchKernelGGL(muon_update_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
   NSH_LAUNCHED();
   return 0;

@@ -156,10 +156,59 @@ __global__ __launch_bounds__(256) void layernorm_grad_kernel(const float* __rest
   for (int c = lane; c < last; c += 64) o[c] = (dr[c] - md - (xr[c] - mx) * gamma) * inv;
 }
 
+// The same formula with both rows held in registers (NV float4 per lane,
+// up to 256*NV columns): x and d are read once and dx written once.
+template <int NV>
+__global__ __launch_bounds__(256) void layernorm_grad_vec_kernel(const float* __restrict__ dout,
+                                                                 const float* __restrict__ x,
+                                                                 float* __restrict__ dx, int64_t rows, int last) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const gfloat* xr = as_global(x + r * last);
+  const gfloat* dr = as_global(dout + r * last);
+  fvec4 xv[NV], dv[NV];
+  float sx = 0.f, sd = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c = (lane + 64 * i) * 4;
+    const bool in = c < last;
+    xv[i] = in ? *(const gfloat4*)(xr + c) : fvec4{0.f, 0.f, 0.f, 0.f};
+    dv[i] = in ? *(const gfloat4*)(dr + c) : fvec4{0.f, 0.f, 0.f, 0.f};
+    sx += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+    sd += (dv[i].x + dv[i].y) + (dv[i].z + dv[i].w);
+  }
+  const float mx = wave_sum(sx) / (float)last;
+  const float md = wave_sum(sd) / (float)last;
+  float sv = 0.f, sg = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    if ((lane + 64 * i) * 4 < last) {
+      const fvec4 a = xv[i] - mx;
+      sv += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+      sg += (a.x * dv[i].x + a.y * dv[i].y) + (a.z * dv[i].z + a.w * dv[i].w);
+    }
+  }
+  const float var = wave_sum(sv) / (float)last;
+  const float gamma = wave_sum(sg) / (float)last;
+  const float inv = 1.f / sqrtf(var + 1e-5f);
+  gfloat* o = as_global(dx + r * last);
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c = (lane + 64 * i) * 4;
+    if (c < last) *(gfloat4*)(o + c) = (dv[i] - md - (xv[i] - mx) * gamma) * inv;
+  }
+}
+
 int launch_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last, hipStream_t s) {
   if (rows <= 0) return 0;
-  hipLaunchKernelGGL(layernorm_grad_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, dout, x, dx, rows,
-                     (int)last);
+  const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
+  const bool vec = last % 4 == 0 && ((uintptr_t)dout | (uintptr_t)x | (uintptr_t)dx) % 16 == 0;
+  const int L = (int)last;
+  if (vec && last <= 256) hipLaunchKernelGGL(layernorm_grad_vec_kernel<1>, grid, block, 0, s, dout, x, dx, rows, L);
+  else if (vec && last <= 512) hipLaunchKernelGGL(layernorm_grad_vec_kernel<2>, grid, block, 0, s, dout, x, dx, rows, L);
+  else if (vec && last <= 1024) hipLaunchKernelGGL(layernorm_grad_vec_kernel<4>, grid, block, 0, s, dout, x, dx, rows, L);
+  else hipLaunchKernelGGL(layernorm_grad_kernel, grid, block, 0, s, dout, x, dx, rows, L);
   NSH_LAUNCHED();
   return 0;
 }
@@ -300,16 +349,29 @@ __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __re
   if (t == 0) row_loss[r] = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
 }
 
-// Deterministic single-workgroup sum of row losses / rows.
-__global__ __launch_bounds__(256) void mean_loss_kernel(const float* __restrict__ row_loss, int64_t rows,
-                                                        float* __restrict__ out) {
-  __shared__ float part[4];
+// Deterministic single-workgroup sum of row losses / rows: 1024 threads,
+// each summing 4 consecutive losses per step (float4 where the buffer is
+// 16-byte aligned), then a fixed tree over the 16 waves.
+__global__ __launch_bounds__(1024) void mean_loss_kernel(const float* __restrict__ row_loss, int64_t rows,
+                                                         float* __restrict__ out) {
+  __shared__ float part[16];
+  const gfloat* rl = as_global(row_loss);
+  const int64_t n4 = ((uintptr_t)row_loss % 16 == 0) ? rows / 4 : 0;
   float s = 0.f;
-  for (int64_t i = threadIdx.x; i < rows; i += 256) s += row_loss[i];
+  for (int64_t i = threadIdx.x; i < n4; i += 1024) {
+    const fvec4 v = ((const gfloat4*)rl)[i];
+    s += (v.x + v.y) + (v.z + v.w);
+  }
+  for (int64_t i = 4 * n4 + threadIdx.x; i < rows; i += 1024) s += rl[i];
   s = wave_sum(s);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
   __syncthreads();
-  if (threadIdx.x == 0) out[0] = ((part[0] + part[1]) + (part[2] + part[3])) / (float)rows;
+  if (threadIdx.x == 0) {
+    float t[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) t[k] = part[2 * k] + part[2 * k + 1];
+    out[0] = (((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]))) / (float)rows;
+  }
 }
 
 int launch_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
@@ -333,7 +395,7 @@ int launch_softmax_xent(const float* logits, const float* labels, float* grad, f
     hipLaunchKernelGGL(softmax_xent_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, s, logits, labels, grad,
                        row_loss, rows, C, write_grad ? 1 : 0);
   NSH_LAUNCHED();
-  hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(256), 0, s, row_loss, rows, loss);
+  hipLaunchKernelGGL(mean_loss_kernel, dim3(1), dim3(1024), 0, s, row_loss, rows, loss);
   NSH_LAUNCHED();
   return 0;
 }

@@ -690,8 +690,19 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
   const int nm = (int)m->muon_host.size();
   MuonMat* d = reinterpret_cast<MuonMat*>(scratch(m, "muon_desc", (nm * sizeof(MuonMat) + 3) / 4));
   if (!d) return -1;
-  Prof p(m, "muon");
-  return muon_batch(d, m->muon_host, max_elems, s);
+  // the three phases as separate profile regions: the transposes are
+  // HBM-bound, the MGS launches latency-bound
+  NSH_CHECK(hipMemcpyAsync(d, m->muon_host.data(), nm * sizeof(MuonMat), hipMemcpyHostToDevice, s));
+  {
+    Prof p(m, "muon_gather");
+    if (launch_muon_gather(d, nm, max_elems, s) != 0) return -1;
+  }
+  {
+    Prof p(m, "muon_mgs");
+    if (launch_mgs(d, m->muon_host.data(), nm, s) != 0) return -1;
+  }
+  Prof p(m, "muon_update");
+  return launch_muon_update(d, nm, max_elems, s);
 }
 
 // Class count of CROSS_ENTROPY / LOSS_GRAD: the logits' static columns

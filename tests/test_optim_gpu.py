@@ -38,30 +38,44 @@ def test_orthonormalize_matches_oracle_mgs(r, c):
     helpers.assert_close(got, ref, f"mgs {r}x{c}", atol=1e-5, rtol=1e-3)
 
 
-@pytest.mark.parametrize("r,c", [(16, 12), (24, 16), (16, 40)])
-def test_muon_step_matches_oracle(r, c):
+def shifted(a, off):
+    """A device copy of `a` starting `off` floats into its buffer (off = 1
+    leaves the data 4 bytes past a 16-byte boundary)."""
+    d = DA.from_host(np.concatenate([np.zeros(off, np.float32), a]))
+    return d, d.ptr + 4 * off
+
+
+# float4 transposes with ragged 64 x 64 tiles (r, c multiples of 4), the
+# scalar 32 x 32 path (r or c odd, or a base off 16-byte alignment), and the
+# row-vector (r < c) copies of both kinds
+@pytest.mark.parametrize("r,c,off", [(16, 12, 0), (24, 16, 0), (16, 40, 0), (200, 72, 0), (72, 200, 0),
+                                     (18, 12, 0), (12, 42, 0), (200, 72, 1), (72, 200, 1)])
+def test_muon_step_matches_oracle(r, c, off):
     w = synth.normal(1, r * c, 0.2)
     g = synth.normal(2, r * c, 0.5)
-    dw, dg, dws = DA.from_host(w), DA.from_host(g), ws(r, c)   # keep the buffers alive across the call
-    runtime.lib().nsh_op_muon_step(dw.ptr, dg.ptr, r, c, ctypes.c_float(0.02), dws.ptr)
+    (dw, pw), (dg, pg), dws = shifted(w, off), shifted(g, off), ws(r, c)  # buffers live across the call
+    runtime.lib().nsh_op_muon_step(pw, pg, r, c, ctypes.c_float(0.02), dws.ptr)
     ref = w.copy()
     oracle.lib().or_muon_step(oracle.fp(ref), oracle.fp(g.copy()), r, c, ctypes.c_float(0.02))
-    helpers.assert_close(dw.to_host(), ref, "muon step")
+    helpers.assert_close(dw.to_host()[off:], ref, "muon step")
 
 
-def test_adamw_steps_are_bit_exact_given_the_gradient():
-    n = 1000
+# float4 path with and without an n % 4 tail, one-element path (n < 4 or a
+# base off 16-byte alignment)
+@pytest.mark.parametrize("n,off", [(1000, 0), (1003, 0), (3, 0), (1003, 1), (262147, 0)])
+def test_adamw_steps_are_bit_exact_given_the_gradient(n, off):
     w = synth.normal(3, n)
-    dw, dm, dv = DA.from_host(w), DA.from_host(np.zeros(n, np.float32)), DA.from_host(np.zeros(n, np.float32))
+    z = np.zeros(n, np.float32)
+    (dw, pw), (dm, pm), (dv, pv) = shifted(w, off), shifted(z, off), shifted(z, off)
     rw, rm, rv = w.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
     for t in range(1, 6):
         g = synth.normal(10 + t, n)
-        dg = DA.from_host(g)
-        runtime.lib().nsh_op_adamw_step(dw.ptr, dg.ptr, dm.ptr, dv.ptr, n, t, ctypes.c_float(0.01))
+        dg, pg = shifted(g, off)
+        runtime.lib().nsh_op_adamw_step(pw, pg, pm, pv, n, t, ctypes.c_float(0.01))
         oracle.lib().or_adamw_step(oracle.fp(rw), oracle.fp(g), oracle.fp(rm), oracle.fp(rv), n, t,
                                    ctypes.c_float(0.01))
-    assert helpers.bitwise_equal(dw.to_host(), rw)
-    assert helpers.bitwise_equal(dm.to_host(), rm) and helpers.bitwise_equal(dv.to_host(), rv)
+    assert helpers.bitwise_equal(dw.to_host()[off:], rw)
+    assert helpers.bitwise_equal(dm.to_host()[off:], rm) and helpers.bitwise_equal(dv.to_host()[off:], rv)
 
 
 @pytest.mark.parametrize("shapes", [[(16, 12), (24, 16), (16, 40)],

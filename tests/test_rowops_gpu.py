@@ -32,7 +32,10 @@ def test_layernorm_forward(rows, last):
     helpers.assert_close(y.to_host(), oracle.layernorm(x, last), f"layernorm {rows}x{last}")
 
 
-@pytest.mark.parametrize("rows,last", [(50, 64), (4096, 512), (3, 1000)])
+# rows in registers (up to 256, 512, 1024 columns, ragged ones included) and
+# the streaming kernel (wider rows, or widths off a multiple of 4)
+@pytest.mark.parametrize("rows,last", [(50, 64), (77, 96), (5, 300), (4096, 512), (3, 1000), (1000, 1024),
+                                       (37, 2048), (9, 7)])
 def test_layernorm_backward(rows, last):
     x = synth.normal(rows + 1, rows * last, 1.5)
     d = synth.normal(rows + 2, rows * last, 0.1)
@@ -41,7 +44,8 @@ def test_layernorm_backward(rows, last):
     helpers.assert_close(dx.to_host(), oracle.layernorm_grad(d, x, last), f"layernorm_grad {rows}x{last}")
 
 
-@pytest.mark.parametrize("rows,C", [(1, 2), (129, 10), (512, 8192), (64, 2048), (33, 4000), (7, 12288), (5, 2050)])
+@pytest.mark.parametrize("rows,C", [(1, 2), (129, 10), (512, 8192), (64, 2048), (33, 4000), (7, 12288), (5, 2050),
+                                    (16387, 16)])
 def test_softmax_cross_entropy_and_seed(rows, C):
     x = synth.normal(rows + C, rows * C, 3.0)
     y = synth.one_hot(synth.token_ids(rows, rows, C), C)
