@@ -52,28 +52,58 @@ struct TileLayout<false, ROWS> {  // [k][rows], rows contiguous
 //  KC: element (row, k) at base[row*ld + k]   (k contiguous)
 //  MC: element (row, k) at base[k*ld + row]   (row contiguous)
 // `rows` = extent of the row dimension (M or N), `K` = contraction extent.
+// init() resolves what stays fixed over the K loop: with VEC, each thread's
+// load addresses at k = 0 (row maps looked up once), so a slab's load is one
+// add per float4; load<CHK = false> is for tiles whose rows and K slabs are
+// all in range (no per-element checks).
 template <bool KC, bool VEC, int ROWS, int NTH>
 struct Stage {
   static constexpr int kVec = ROWS * BK / 4 / NTH;  // float4 per thread (VEC)
   static constexpr int kSca = ROWS * BK / NTH;      // floats per thread
+  static constexpr int kPtr = VEC ? kVec : 1;
   float v[kSca];
+  const float* p[kPtr];
+  unsigned rin;  // VEC: bit i set = the rows of load i are in range
+  // the arguments (the scalar path resolves them per element)
+  const float* base_;
+  const int* rmap_;
+  int row0_, rows_;
+
+  __device__ static void vec_pos(int idx, int& r, int& k) {
+    if (KC) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; } else { k = idx / (ROWS / 4); r = (idx % (ROWS / 4)) * 4; }
+  }
   // rmap (optional): row r of the operand is row rmap[r] of `base`.
-  __device__ void load(const float* __restrict__ base, int64_t ld, int row0, int rows, int k0, int K,
-                       int t, const int* __restrict__ rmap = nullptr) {
+  __device__ void init(const float* __restrict__ base, int64_t ld, int row0, int rows, int t,
+                       const int* __restrict__ rmap = nullptr) {
+    base_ = base, rmap_ = rmap, row0_ = row0, rows_ = rows;
     if (VEC) {
+      rin = 0;
+#pragma unroll
+      for (int i = 0; i < kPtr; i++) {
+        int r, k;
+        vec_pos(t + NTH * i, r, k);
+        const int gr = row0 + r;
+        const bool in = gr < rows;
+        rin |= in ? 1u << i : 0u;  // whole float4 in or out: the contiguous extent is a multiple of 4
+        const int64_t rr = !in ? 0 : rmap ? (int64_t)rmap[gr] : (int64_t)gr;
+        p[i] = KC ? base + rr * ld + k : base + (int64_t)k * ld + (in ? gr : 0);
+      }
+    }
+  }
+  template <bool CHK = true>
+  __device__ void load(int64_t ld, int k0, int K, int t) {
+    if (VEC) {
+      const int64_t off = KC ? (int64_t)k0 : (int64_t)k0 * ld;
 #pragma unroll
       for (int i = 0; i < kVec; i++) {
-        const int idx = t + NTH * i;
-        int r, k;
-        if (KC) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; } else { k = idx / (ROWS / 4); r = (idx % (ROWS / 4)) * 4; }
-        const int gr = row0 + r, gk = k0 + k;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        // Whole float4 in or out: the contiguous extent is a multiple of 4.
-        if (gr < rows && gk < K) {
-          const int64_t rr = rmap ? (int64_t)rmap[gr] : (int64_t)gr;
-          const float* p = KC ? base + rr * ld + gk : base + (int64_t)gk * ld + gr;
-          x = *reinterpret_cast<const float4*>(p);
+        bool ok = true;
+        if (CHK) {
+          int r, k;
+          vec_pos(t + NTH * i, r, k);
+          ok = ((rin >> i) & 1) && k0 + k < K;
         }
+        if (ok) x = *reinterpret_cast<const float4*>(p[i] + off);
         v[4 * i + 0] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
       }
     } else {
@@ -82,11 +112,11 @@ struct Stage {
         const int idx = t + NTH * i;
         int r, k;
         if (KC) { r = idx / BK; k = idx % BK; } else { k = idx / ROWS; r = idx % ROWS; }
-        const int gr = row0 + r, gk = k0 + k;
+        const int gr = row0_ + r, gk = k0 + k;
         float x = 0.f;
-        if (gr < rows && gk < K) {
-          const int64_t rr = rmap ? (int64_t)rmap[gr] : (int64_t)gr;
-          x = KC ? base[rr * ld + gk] : base[(int64_t)gk * ld + gr];
+        if (!CHK || (gr < rows_ && gk < K)) {
+          const int64_t rr = rmap_ ? (int64_t)rmap_[gr] : (int64_t)gr;
+          x = KC ? base_[rr * ld + gk] : base_[(int64_t)gk * ld + gr];
         }
         v[i] = x;
       }
@@ -217,21 +247,32 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
   Stage<AKC, VEC, BMT, NTT> sa;
   Stage<BKC, VEC, BNT, NTT> sb;
   const int nk = (kend - kbeg + BK - 1) / BK;
-  sa.load(A, lda, m0, m_end, kbeg, kend, t, g.a_rows);
-  sb.load(B, ldb, n0, N, kbeg, kend, t);
+  // (the 256-row tiles never gather rows)
+  sa.init(A, lda, m0, m_end, t, WMW == 2 ? nullptr : g.a_rows);
+  sb.init(B, ldb, n0, N, t);
+  sa.load(lda, kbeg, kend, t);
+  sb.load(ldb, kbeg, kend, t);
   sa.store(smem, t);
   sb.store(smem + ASZ, t);
   __syncthreads();
+  // every row and K slab of the tile in range: loads without checks
+  const bool full = m0 + BMT <= m_end && n0 + BNT <= N && (kend - kbeg) % BK == 0;
 
   for (int kt = 0; kt < nk; kt++) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nk;
     if (more) {
-      sa.load(A, lda, m0, m_end, kbeg + (kt + 1) * BK, kend, t, g.a_rows);
-      sb.load(B, ldb, n0, N, kbeg + (kt + 1) * BK, kend, t);
+      if (full) {
+        sa.template load<false>(lda, kbeg + (kt + 1) * BK, kend, t);
+        sb.template load<false>(ldb, kbeg + (kt + 1) * BK, kend, t);
+      } else {
+        sa.load(lda, kbeg + (kt + 1) * BK, kend, t);
+        sb.load(ldb, kbeg + (kt + 1) * BK, kend, t);
+      }
     }
     const float* as = smem + cur * (ASZ + BSZ);
     const float* bs = as + ASZ;
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int g = 0; g < 2; g++) {
       const int kb = 8 * g + 4 * kh;
@@ -248,6 +289,7 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
           for (int c = 0; c < 2; c++)
             acc[r][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[r][q], fb[c][q], acc[r][c], 0, 0, 0);
     }
+    __builtin_amdgcn_s_setprio(0);
     if (more) {
       float* nxt = smem + (cur ^ 1) * (ASZ + BSZ);
       sa.store(nxt, t);
