@@ -69,11 +69,11 @@ struct Stage {
   const int* rmap_;
   int row0_, rows_;
 
-  __device__ static void vec_pos(int idx, int& r, int& k) {
+  __device__ __forceinline__ static void vec_pos(int idx, int& r, int& k) {
     if (KC) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; } else { k = idx / (ROWS / 4); r = (idx % (ROWS / 4)) * 4; }
   }
   // rmap (optional): row r of the operand is row rmap[r] of `base`.
-  __device__ void init(const float* __restrict__ base, int64_t ld, int row0, int rows, int t,
+  __device__ __forceinline__ void init(const float* __restrict__ base, int64_t ld, int row0, int rows, int t,
                        const int* __restrict__ rmap = nullptr) {
     base_ = base, rmap_ = rmap, row0_ = row0, rows_ = rows;
     if (VEC) {
@@ -91,7 +91,7 @@ struct Stage {
     }
   }
   template <bool CHK = true>
-  __device__ void load(int64_t ld, int k0, int K, int t) {
+  __device__ __forceinline__ void load(int64_t ld, int k0, int K, int t) {
     if (VEC) {
       const int64_t off = KC ? (int64_t)k0 : (int64_t)k0 * ld;
 #pragma unroll
@@ -122,7 +122,7 @@ struct Stage {
       }
     }
   }
-  __device__ void store(float* __restrict__ lds, int t) const {
+  __device__ __forceinline__ void store(float* __restrict__ lds, int t) const {
     if (VEC) {
 #pragma unroll
       for (int i = 0; i < kVec; i++) {
@@ -346,22 +346,45 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
       }
     return;
   }
+  // General epilogue (row scatter, row scale, activation gradient or
+  // accumulate).  The rows a lane holds in a 32-row block share their output
+  // row and scale between the two column blocks: they are looked up once,
+  // eight rows at a time with all eight loads in flight together.
 #pragma unroll
   for (int r = 0; r < 2; r++)
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-      const int col = n0 + wn * 64 + c * 32 + l32;
-      if (col >= N) continue;
+    for (int h = 0; h < 2; h++) {
+      const int rbase = m0 + wm * 64 + r * 32 + 16 * h + 4 * kh;
+      int crow[8];
+      float rs[8];
+      // rows past m_end read row m_end - 1's entries (m0 < m_end) and are
+      // then marked -1: the loads carry no branch and issue together
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int row = m0 + wm * 64 + r * 32 + 8 * (v >> 2) + 4 * kh + (v & 3);
-        if (row >= m_end) continue;
-        const int64_t crow = g.c_rows ? (int64_t)g.c_rows[row] : (int64_t)row;
-        float* dst = C + crow * ldc + col;
-        const float a = g.row_scale ? acc[r][c][v] * g.row_scale[crow] : acc[r][c][v];
-        if (g.mode == kEpiAct) *dst = act_apply(a, g.act);
-        else if (g.mode == kEpiActGrad) *dst = a * act_deriv(g.aux[(int64_t)row * g.ldaux + col], g.act);
-        else *dst = *dst + a;
+      for (int u = 0; u < 8; u++) crow[u] = min(rbase + 8 * (u >> 2) + (u & 3), m_end - 1);
+      if (g.c_rows) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) crow[u] = g.c_rows[crow[u]];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) rs[u] = g.row_scale ? g.row_scale[crow[u]] : 1.f;
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (rbase + 8 * (u >> 2) + (u & 3) >= m_end) crow[u] = -1;
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const int col = n0 + wn * 64 + c * 32 + l32;
+        if (col >= N) continue;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          if (crow[u] < 0) continue;
+          const int row = rbase + 8 * (u >> 2) + (u & 3);
+          float* dst = C + (int64_t)crow[u] * ldc + col;
+          const float x = acc[r][c][8 * h + u];
+          const float a = g.row_scale ? x * rs[u] : x;
+          if (g.mode == kEpiAct) *dst = act_apply(a, g.act);
+          else if (g.mode == kEpiActGrad) *dst = a * act_deriv(g.aux[(int64_t)row * g.ldaux + col], g.act);
+          else *dst = *dst + a;
+        }
       }
     }
 }
@@ -383,6 +406,10 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   // plain epilogue: no row maps or scaling; activation, accumulate or the
   // pre-activation / activation pair (kchunk partials are always kEpiAct)
   const bool plain = !g.c_rows && !g.row_scale && (g.mode == kEpiAct || g.mode == kEpiAccum);
+  if (g.C2 && !(plain && g.mode == kEpiAct)) {
+    set_error("gemm: the pre-activation / activation pair needs the plain activation epilogue");
+    return -1;
+  }
   // 256-row tiles for large dense plain NN products; 256-column tiles for
   // the grouped (per-expert) NN products, whose row ranges are short
   const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kchunk && !g.a_rows && g.M >= 2048;
