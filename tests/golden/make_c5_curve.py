@@ -6,7 +6,7 @@
 host, computed by the oracle restatement (bit-identical to the reference's
 emitted CPU driver, tests/test_oracle.py pins it), because the reference's
 own single-threaded driver would need hours per step at this size.
-Run in the build container (~2 h on 6 cores):
+Run in the build container (about 5 h on 6 cores):
     OMP_NUM_THREADS=6 python tests/golden/make_c5_curve.py
 """
 import os

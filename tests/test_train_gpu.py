@@ -207,3 +207,29 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     assert not bad, bad
     model.free()
 
+
+def test_c5_full_size_100_step_loss_curve():
+    """Config c5 at full size (one 16384-token sequence, vocab 8192, Muon on
+    every matrix): 100 device-resident training steps with the host's cosine
+    warmup lr (3e-4 x lr_scale(t)) against the oracle's curve, which is
+    bit-identical to the reference's emitted driver (written by
+    tests/golden/make_c5_curve.py): every loss within 1e-3, the first (a pure
+    forward) within fp32 tolerance."""
+    from golden.make_golden import digest
+    from neuralscript_amd import workloads
+    print("c5 full-size curve: 100 steps", flush=True)
+    g = np.load(os.path.join(helpers.GOLDEN, "curve_c5_full.npz"))
+    assert int(g["steps_done"]) == 100
+    plan = runtime.Plan.load("c5")
+    w = workloads.weights("c5", plan.layout(), workloads.ir_shapes(plan.ir))
+    x, y = workloads.inputs("c5"), workloads.labels("c5")
+    assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w_digest"]), "input generator drifted"
+    model = runtime.Model(plan, w)
+    dx, dy = runtime.DeviceArray.from_host(x), runtime.DeviceArray.from_host(y)
+    losses = np.array([model.train_step_device(dx, dy, lr) for lr in curve_lrs(3e-4, 100)], dtype=np.float32)
+    model.free()
+    dev = np.abs(losses.astype(np.float64) - g["losses"])
+    print(f"  max |loss - reference| = {dev.max():.3g} at step {int(dev.argmax())}; "
+          f"losses {losses[0]:.6f} .. {losses[-1]:.6f}")
+    helpers.assert_close(losses[:1], g["losses"][:1], "c5 first loss")
+    assert np.all(dev <= LOSS_TOL), dev
