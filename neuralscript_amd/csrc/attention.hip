@@ -187,7 +187,11 @@ __global__ __launch_bounds__(kFW * 64) void flash_fwd_kernel(const float* __rest
     // prefetch K tile it+2 and V tile it+1 (clamped: the last tiles reload)
     tk.load(K, ld, hcol, min(it + 2, nkv - 1) * kBK, S, t);
     tv.load(V, ld, hcol, min(it + 1, nkv - 1) * kBK, S, t);
+    // MFMA bursts run at raised wave priority, so a SIMD's other wave fills
+    // the gaps with its softmax work rather than competing for issue
+    __builtin_amdgcn_s_setprio(1);
     if (it + 1 < nkv) score_tile<DK>(kbuf + ((it + 1) & 1) * TF, qf, l32, kh, sn);
+    __builtin_amdgcn_s_setprio(0);
 
     // Online softmax for this lane's query (keys 8*(v/4) + 4kh + v%4 of each block).
     const int kbase = it * kBK;
@@ -229,6 +233,7 @@ __global__ __launch_bounds__(kFW * 64) void flash_fwd_kernel(const float* __rest
     m = mnew;
 
     // O^T += V^T P^T: step s of key block kb pairs key 8*(s/4)+4kh+s%4.
+    __builtin_amdgcn_s_setprio(1);
     const float* vs = vbuf + (it & 1) * TF;
 #pragma unroll
     for (int kb = 0; kb < 2; kb++)
@@ -239,6 +244,7 @@ __global__ __launch_bounds__(kFW * 64) void flash_fwd_kernel(const float* __rest
         for (int d = 0; d < NDB; d++)
           o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key * P + d * 32 + l32], sc[kb][s], o[d], 0, 0, 0);
       }
+    __builtin_amdgcn_s_setprio(0);
 
     // K tile it (consumed last iteration) and V tile it-1 (consumed last
     // iteration) are free: fill them with K tile it+2 and V tile it+1.
@@ -432,6 +438,8 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
       floatx16 sc, dp;
 #pragma unroll
       for (int v = 0; v < 16; v++) { sc[v] = 0.f; dp[v] = 0.f; }
+      // MFMA phases at raised wave priority (as in the forward)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int g = 0; g < DK / 8; g++) {
         const float4 qa = *reinterpret_cast<const float4*>(qs + (qb * 32 + l32) * Tile::P + 8 * g + 4 * kh);
@@ -445,6 +453,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
         dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.z, vf[4 * g + 2], dp, 0, 0, 0);
         dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga.w, vf[4 * g + 3], dp, 0, 0, 0);
       }
+      __builtin_amdgcn_s_setprio(0);
       // element v: query qb*32 + 8(v/4) + 4kh + v%4, key = this lane's
 #pragma unroll
       for (int v = 0; v < 16; v++) {
@@ -470,6 +479,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
           dst += 4 * (int64_t)S;
         }
       }
+      __builtin_amdgcn_s_setprio(1);
       // dV += P^T dO, dK += dS^T Q: step s pairs query 8(s/4) + 4kh + s%4.
 #pragma unroll
       for (int s = 0; s < 16; s++) {
@@ -481,6 +491,7 @@ __global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __r
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (more) tile.store(sm + (cur ^ 1) * Tile::kFloats, t);
     __syncthreads();
   }
