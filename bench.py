@@ -151,6 +151,13 @@ def bench_forward(key, steps, warmup):
     model.sync()
     dt = time.perf_counter() - t0
     prof = model.profile_report()
+    model.profile(False)
+    # host-pointer ABI (ns_eval_infer: PCIe copies included), for reference
+    model.eval_infer(x)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        model.eval_infer(x)
+    abi_dt = (time.perf_counter() - t0) / 3
     routing = None
     if key == "c4":
         E = workloads.ir_shapes(plan.ir)["moe_g_w"][1]
@@ -176,6 +183,8 @@ def bench_forward(key, steps, warmup):
            "roofline": roofline_of(key, region, work[region],
                                    prof[region]["ms"] / prof[region]["calls"]),
            "kernels": kernels}
+    out["host_abi"] = {"tokens_per_s": wl.rows / abi_dt, "ms": abi_dt * 1e3,
+                       "note": "ns_eval_infer with host buffers (PCIe-inclusive)"}
     if routing is not None:
         out["routing"] = routing
     return out
@@ -251,7 +260,17 @@ def bench_train(key, steps, warmup):
     model.sync()
     dt = time.perf_counter() - t0
     prof = model.profile_report()
+    model.profile(False)
     loss = model.train_step_device(dx, dy, 3e-4 * scale(t))
+    t += 1
+    # host-pointer ABI (ns_runtime_train_step: the [M, C] one-hot labels cross
+    # PCIe every call), for reference
+    xh, yh = workloads.inputs(key), workloads.labels(key)
+    t0 = time.perf_counter()
+    for _ in range(2):
+        model.train_step(xh, yh, 3e-4 * scale(t))
+        t += 1
+    abi_dt = (time.perf_counter() - t0) / 2
     model.free()
     work = c5_work()
     shapes = workloads.ir_shapes(plan.ir)
@@ -273,7 +292,9 @@ def bench_train(key, steps, warmup):
             "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device"},
             "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
             "roofline": roofline_of(key, "attention_bwd", work["attention_bwd"], att["ms"] / att["calls"]),
-            "kernels": kernels, "adamw": adamw_bandwidth(n_muon)}
+            "kernels": kernels, "adamw": adamw_bandwidth(n_muon),
+            "host_abi": {"steps_per_s": 1.0 / abi_dt, "ms": abi_dt * 1e3,
+                         "note": "ns_runtime_train_step with host buffers (labels uploaded every call)"}}
 
 
 def bench_c2(steps, warmup, with_cpu):
@@ -339,8 +360,75 @@ def bench_c2(steps, warmup, with_cpu):
         "host_abi": {"tokens_per_s": rows / abi_dt, "note": "ns_eval_infer with host buffers (PCIe-inclusive)"},
     }
     model.free()
+    res["measured_peak"] = measured_peaks()
+    res["roofline"]["frac_of_measured_peak"] = achieved / res["measured_peak"]["mfma_f32_tflops"]
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline_c2()
+    return res
+
+
+def measured_peaks():
+    """Attainable peaks of this GPU, measured by libnship's microbenchmarks:
+    a register-only fp32 MFMA loop (2048 workgroups x 4 waves, 4 independent
+    32x32x2 chains per wave) and a float4 copy of 256 MiB each way."""
+    import ctypes
+    from neuralscript_amd import runtime
+    lib = runtime.lib()
+    tf = ctypes.c_double()
+    runtime.check(lib.nsh_bench_mfma_peak(4000, 2048, ctypes.byref(tf)), "bench_mfma_peak")
+    n = 1 << 26
+    src, dst = runtime.DeviceArray(n), runtime.DeviceArray(n)
+    src.fill_zero()
+    dst.fill_zero()
+    gbs = ctypes.c_double()
+    runtime.check(lib.nsh_bench_copy(src.ptr, dst.ptr, n, 10, ctypes.byref(gbs)), "bench_copy")
+    src.free()
+    dst.free()
+    return {"mfma_f32_tflops": tf.value, "mfma_frac_of_published": tf.value / MFMA_F32_PEAK_TFLOPS,
+            "hbm_copy_gbs": gbs.value, "hbm_frac_of_published": gbs.value / HBM_PEAK_GBS}
+
+
+def library_gemm(M=8192, N=4096, K=4096, reps=20):
+    """The vendor library's fp32 GEMM (torch.mm -> hipBLASLt / rocBLAS, no
+    reduced-precision modes) on c2's 4096x4096 layer, for comparison only."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    a = torch.randn(M, K, device="cuda", dtype=torch.float32)
+    b = torch.randn(K, N, device="cuda", dtype=torch.float32)
+    for _ in range(3):
+        c = torch.mm(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        c = torch.mm(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del c
+    return {"shape": [M, N, K], "ms": ms, "TFLOP/s": 2.0 * M * N * K / (ms * 1e-3) / 1e12,
+            "torch": torch.__version__}
+
+
+def bench_peak():
+    """--config peak: the attainable peaks and the vendor library's fp32 GEMM
+    next to libnship's on the same shape."""
+    from neuralscript_amd import runtime
+    res = {"measured_peak": measured_peaks()}
+    M, N, K = 8192, 4096, 4096
+    A, B, C = runtime.DeviceArray(M * K), runtime.DeviceArray(K * N), runtime.DeviceArray(M * N)
+    for d in (A, B, C):
+        d.fill_zero()
+    for _ in range(3):
+        runtime.op("gemm", A, B, C, M, N, K, K, N, N, 0, 0, 0)
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        runtime.op("gemm", A, B, C, M, N, K, K, N, N, 0, 0, 0)
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    res["libnship_gemm"] = {"shape": [M, N, K], "ms": ms, "TFLOP/s": 2.0 * M * N * K / (ms * 1e-3) / 1e12,
+                            "note": "nsh_op_gemm, synchronous per call (host-timed)"}
+    res["library_gemm"] = library_gemm(M, N, K)
     return res
 
 
@@ -365,9 +453,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "copy"],
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "copy", "peak"],
                     help="c2 (default) is the metric's workload; c3/c4 (forward) and c5 (training steps) "
-                         "print per-kernel breakdowns; copy runs the rocprof counter calibration copy")
+                         "print per-kernel breakdowns; copy runs the rocprof counter calibration copy; peak "
+                         "measures the attainable MFMA / HBM peaks and the vendor library's fp32 GEMM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -375,6 +464,8 @@ def main():
                          "--gpus must be 1)")
     if a.config == "copy":
         res = copy_calibration()
+    elif a.config == "peak":
+        res = bench_peak()
     elif a.config == "c2":
         res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
     elif a.config == "c5":

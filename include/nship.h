@@ -197,6 +197,15 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
  * place; codegen.cpp:3108-3119. */
 int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr);
 
+/* Attainable peaks of the running GPU (no reference counterpart: the
+ * reference has no timing).  nsh_bench_mfma_peak: register-only fp32 MFMA
+ * loop, blocks x 256 threads, iters x 4 MFMA 32x32x2 per wave (4096 FLOP
+ * each); *tflops = executed rate.  nsh_bench_copy: float4 copy of n floats
+ * (n % 4 == 0, 16-byte aligned), mean over reps; *gbs = (read + write)
+ * bytes / time. */
+int nsh_bench_mfma_peak(int iters, int blocks, double* tflops);
+int nsh_bench_copy(const float* src, float* dst, int64_t n, int reps, double* gbs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,6 +112,14 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
 int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s);
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 
+// peak.hip -----------------------------------------------------------------------
+// Attainable-peak microbenchmarks: time (ms, HIP events on the null stream) of
+// one launch of `blocks` x 256 threads issuing iters x 4 fp32 MFMAs per wave,
+// and of one float4 copy of n floats (mean over reps); `out` is a dummy
+// buffer of 256 floats.
+int bench_mfma_peak(int iters, int blocks, float* out, float* ms);
+int bench_copy(const float* src, float* dst, int64_t n, int reps, float* ms);
+
 // movement.hip -------------------------------------------------------------------
 int launch_binop(const float* A, const float* B, float* C, int64_t na, int64_t nb, int code, hipStream_t s);
 // out = in, then softmax over each full row of `last` (a tail shorter than a row is copied)

@@ -1599,6 +1599,32 @@ int nsh_op_muon_step(float* w, const float* g, int64_t r, int64_t c, float lr, v
   return op_muon(w, g, r, c, lr * sqrtf((float)std::min(r, c)), 0.01f * lr, workspace);
 }
 
+int nsh_bench_mfma_peak(int iters, int blocks, double* tflops) {
+  if (iters <= 0 || blocks <= 0 || !tflops) {
+    set_error("bench_mfma_peak: bad arguments");
+    return -1;
+  }
+  float* out = nullptr;
+  NSH_CHECK(hipMalloc(&out, 256 * sizeof(float)));
+  float ms = 0.f;
+  const int rc = bench_mfma_peak(iters, blocks, out, &ms);
+  hipFree(out);
+  if (rc != 0) return -1;
+  *tflops = (double)blocks * 4 * iters * 4 * 4096.0 / (ms * 1e-3) / 1e12;
+  return 0;
+}
+
+int nsh_bench_copy(const float* src, float* dst, int64_t n, int reps, double* gbs) {
+  if (!src || !dst || n <= 0 || n % 4 || reps <= 0 || !gbs || (((uintptr_t)src | (uintptr_t)dst) & 15)) {
+    set_error("bench_copy: bad arguments");
+    return -1;
+  }
+  float ms = 0.f;
+  if (bench_copy(src, dst, n, reps, &ms) != 0) return -1;
+  *gbs = 2.0 * (double)n * 4 / (ms * 1e-3) / 1e9;
+  return 0;
+}
+
 int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr) {
   const float b1t = 1.f - powf(0.9f, (float)t), b2t = 1.f - powf(0.999f, (float)t);
   if (launch_adamw(w, g, m, v, n, lr, b1t, b2t, nullptr) != 0) return -1;
