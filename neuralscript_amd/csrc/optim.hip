@@ -97,11 +97,11 @@ __device__ __forceinline__ bool vec4_ok(int64_t R, int64_t C, const void* a, con
 
 // T = the vectors of g, contiguous: r < c, the rows (a copy); r >= c, the
 // columns, T[j][k] = g[k][j], transposed through LDS so both sides are read
-// and written along rows: 64 x 64 tiles with float4 on both sides (the LDS
-// row pitch of 65 keeps the column reads conflict-free), or 32 x 32 scalar
-// tiles where float4 does not fit.  grid.y = matrix.
+// and written along rows: 64 x 128 tiles with float4 on both sides (the odd
+// LDS row pitch of 129 keeps the column reads conflict-free), or 32 x 32
+// scalar tiles where float4 does not fit.  grid.y = matrix.
 __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restrict__ mats, int nmat) {
-  __shared__ float tile[64 * 65];
+  __shared__ float tile[64 * 129];
   const MuonMat& M = mats[blockIdx.y];
   const gfloat* __restrict__ g = as_global(M.g);
   gfloat* __restrict__ T = as_global(M.T);
@@ -120,28 +120,37 @@ __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restr
     return;
   }
   if (vec) {
-    // thread: float4 column q (of 16 per 64-wide row), rows rr + 16 i
+    // 64 (k) x 128 (j) tiles: each g row segment read is 512 contiguous
+    // bytes and all 8 float4 loads of a thread are in flight together.
+    // Thread: float4 column q (of 16 per 64-wide half row), rows rr + 16 i.
     const int q = threadIdx.x & 15, rr = threadIdx.x >> 4;
-    const int64_t tc = (C + 63) / 64, tiles = ((R + 63) / 64) * tc;
+    const int64_t tc = (C + 127) / 128, tiles = ((R + 63) / 64) * tc;
     for (int64_t b = blockIdx.x; b < tiles; b += gridDim.x) {
-      const int64_t k0 = (b / tc) * 64, j0 = (b % tc) * 64;
+      const int64_t k0 = (b / tc) * 64, j0 = (b % tc) * 128;
+      fvec4 x[4][2];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = rr + 16 * i;
-        if (k0 + r < R && j0 + 4 * q < C) {
-          const fvec4 x = *(const gfloat4*)(g + (k0 + r) * C + j0 + 4 * q);
-          float* t = tile + r * 65 + 4 * q;
-          t[0] = x.x, t[1] = x.y, t[2] = x.z, t[3] = x.w;
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          const int r = rr + 16 * i, jc = 64 * hh + 4 * q;
+          x[i][hh] = (k0 + r < R && j0 + jc < C) ? *(const gfloat4*)(g + (k0 + r) * C + j0 + jc)
+                                                 : fvec4{0.f, 0.f, 0.f, 0.f};
         }
-      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+          float* t = tile + (rr + 16 * i) * 129 + 64 * hh + 4 * q;
+          t[0] = x[i][hh].x, t[1] = x[i][hh].y, t[2] = x[i][hh].z, t[3] = x[i][hh].w;
+        }
       __syncthreads();
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
+      for (int i = 0; i < 8; i++) {
         const int jj = rr + 16 * i;
         if (j0 + jj < C && k0 + 4 * q < R) {
-          const float* t = tile + 4 * q * 65 + jj;
+          const float* t = tile + 4 * q * 129 + jj;
           fvec4 y;
-          y.x = t[0], y.y = t[65], y.z = t[130], y.w = t[195];
+          y.x = t[0], y.y = t[129], y.z = t[258], y.w = t[387];
           *(gfloat4*)(T + (j0 + jj) * R + k0 + 4 * q) = y;
         }
       }
@@ -513,8 +522,8 @@ int muon_blocks(int C) { return (int)ceil_div(C, kCPB) > 0 ? (int)ceil_div(C, kC
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
-  // one workgroup per 64 x 64 tile of the largest matrix
-  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 4096), 4096);
+  // one workgroup per 64 x 128 tile of the largest matrix
+  const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 8192), 4096);
   hipLaunchKernelGGL(muon_gather_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
   NSH_LAUNCHED();
   return 0;
