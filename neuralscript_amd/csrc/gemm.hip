@@ -273,6 +273,9 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
     const float* as = smem + cur * (ASZ + BSZ);
     const float* bs = as + ASZ;
     __builtin_amdgcn_s_setprio(1);
+    // the scheduler's MFMA / LDS-read interleaving for GEMM loops: +0.5-0.9%
+    // on the 256-row tiles, slower on the others (c5's 128x128 products -21%)
+    if constexpr (WMW == 2) __builtin_amdgcn_iglp_opt(1);
 #pragma unroll
     for (int g = 0; g < 2; g++) {
       const int kb = 8 * g + 4 * kh;
