@@ -49,7 +49,7 @@ def load_traffic(kernel):
         return json.load(f).get(kernel)
 
 
-def cpu_baseline_c2(budget_s=12.0):
+def cpu_baseline_c2(budget_s=15.0):
     """Reference CPU driver (nsc --cpp --runtime, g++ -O2) on a row sample."""
     from neuralscript_amd import runtime, workloads
     from neuralscript_amd.abi import NsLib
@@ -71,11 +71,11 @@ def cpu_baseline_c2(budget_s=12.0):
         om = oracle.Model(oracle.Net(plan.ir), w)
         run = om.eval_infer
         done = lambda: None  # noqa: E731
-    x_all = workloads.inputs("c2", rows=64)
+    x_all = workloads.inputs("c2", rows=160)
     t0 = time.perf_counter()
     run(x_all[:1024])                     # 1 row: calibrates the sample size
     t1 = time.perf_counter() - t0
-    rows = int(max(1, min(64, budget_s / max(t1, 1e-3))))
+    rows = int(max(1, min(160, budget_s / max(t1, 1e-3))))
     t0 = time.perf_counter()
     run(x_all[: rows * 1024])
     dt = time.perf_counter() - t0
