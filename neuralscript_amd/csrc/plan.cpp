@@ -331,7 +331,17 @@ Plan* parse_plan(const char* text, std::string* err) {
         I.heads = h > 0 ? (int)h : 1;
       }
       if (I.op == Op::Moe) {
+        // MoE(initial_experts: K0) lives only in the instruction's ints
+        // attribute (mlir_compiler.cpp:896), which the plain `nsc --mlir`
+        // printer drops (:899-902); without it the liveness mask is unknown,
+        // so the plan is refused rather than assuming every expert live.
+        // K0 <= 0 or > E means all E (mlir_compiler.cpp:194-195).
         const int64_t k0 = comment_int(r.comment, "initial");
+        if (k0 < 0 && r.comment.find("initial=") == std::string::npos) {
+          *err = "ns.layer.moe needs initial=K0 in its comment (the plain nsc --mlir text omits "
+                 "MoE initial_experts; print the IR with oracle/irdump): " + o;
+          return false;
+        }
         MoeInfo& m = P->moe;
         const Value& g = P->vals[I.in[1]];
         const Value& e1 = P->vals[I.in[2]];

@@ -57,6 +57,7 @@ struct ns_model {
   float* d_w = nullptr;
   std::vector<float> h_w;
   bool host_stale = false;  // device blob newer than h_w
+  bool device_stale = false;  // h_w newer than the device blob (a failed upload)
   std::vector<uint8_t> moe_active;
   size_t moe_count = 0;
   uint8_t* d_active = nullptr;
@@ -522,7 +523,10 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
   return -1;
 }
 
+int ensure_device_current(ns_model* m);
+
 int run_forward(ns_model* m, const float* d_x, size_t n_in, float** d_out, size_t* n_out) {
+  if (ensure_device_current(m) != 0) return -1;
   const Plan& P = *m->plan;
   const Func& F = P.fwd;
   Frame fr;
@@ -715,6 +719,7 @@ int64_t ce_classes(const Func& F, const Plan& P, int preds) {
 
 int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, float lr, bool train_mode,
               float** d_loss) {
+  if (ensure_device_current(m) != 0) return -1;
   const Plan& P = *m->plan;
   const Func& F = P.trn;
   hipStream_t s = m->stream;
@@ -968,11 +973,46 @@ int host_sync_weights(const ns_model* m) {
   return 0;
 }
 
-int device_sync_weights(ns_model* m) {
-  NSH_CHECK(hipMemcpy(m->d_w, m->h_w.data(), m->h_w.size() * sizeof(float), hipMemcpyHostToDevice));
-  if (m->d_active && !m->moe_active.empty())
-    NSH_CHECK(hipMemcpy(m->d_active, m->moe_active.data(), m->moe_active.size(), hipMemcpyHostToDevice));
+// Host -> device copies of the host blob and the liveness mask.  They are
+// enqueued on the model's stream, so kernels still running on it (a
+// device-pointer call returns before completion) finish first, and the call
+// waits for them because the host vectors may change right after.  A failed
+// upload marks the device blob stale; the next device call re-uploads it.
+int upload_weights(ns_model* m, size_t off, size_t n) {
+  if (n == 0) return 0;
+  hipError_t e = hipMemcpyAsync(m->d_w + off, m->h_w.data() + off, n * sizeof(float), hipMemcpyHostToDevice,
+                                m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  if (e != hipSuccess) {
+    m->device_stale = true;
+    set_error(std::string("weight upload: ") + hipGetErrorString(e));
+    return -1;
+  }
   return 0;
+}
+
+int upload_mask(ns_model* m) {
+  if (!m->d_active || m->moe_active.empty()) return 0;
+  hipError_t e = hipMemcpyAsync(m->d_active, m->moe_active.data(), m->moe_active.size(), hipMemcpyHostToDevice,
+                                m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  if (e != hipSuccess) {
+    m->device_stale = true;
+    set_error(std::string("mask upload: ") + hipGetErrorString(e));
+    return -1;
+  }
+  return 0;
+}
+
+int device_sync_weights(ns_model* m) {
+  if (upload_weights(m, 0, m->h_w.size()) != 0 || upload_mask(m) != 0) return -1;
+  m->device_stale = false;
+  return 0;
+}
+
+// Before any device work: a lifecycle edit whose upload failed is re-sent.
+int ensure_device_current(ns_model* m) {
+  return m->device_stale ? device_sync_weights(m) : 0;
 }
 
 }  // namespace
@@ -1241,8 +1281,10 @@ size_t nsh_expert_birth(ns_model* m, int n) {
     m->moe_active[(size_t)e] = 1;
     m->moe_count++;
     n--;
+    if (upload_weights(m, o1 + g2, D * H) != 0 || upload_weights(m, o2 + g3, H * D) != 0) return m->moe_count;
   }
-  device_sync_weights(m);
+  // (a failed upload leaves device_stale set: the next device call retries)
+  if (upload_weights(m, og, D * cap) == 0) upload_mask(m);
   return m->moe_count;
 }
 
@@ -1264,7 +1306,9 @@ size_t nsh_expert_merge(ns_model* m, int a, int b) {
     w[o2 + (size_t)a * H * D + t] = 0.5f * (w[o2 + (size_t)a * H * D + t] + w[o2 + (size_t)b * H * D + t]);
   m->moe_active[(size_t)b] = 0;
   m->moe_count--;
-  device_sync_weights(m);
+  if (upload_weights(m, og, D * cap) == 0 && upload_weights(m, o1 + (size_t)a * D * H, D * H) == 0 &&
+      upload_weights(m, o2 + (size_t)a * H * D, H * D) == 0)
+    upload_mask(m);
   return m->moe_count;
 }
 
@@ -1272,9 +1316,11 @@ size_t nsh_expert_kill(ns_model* m, int k) {
   if (!m) return 0;
   const MoeInfo& q = m->plan->moe;
   if (!q.present || k < 0 || k >= (int)q.E || !m->moe_active[(size_t)k]) return m->moe_count;
+  // only the mask changes (codegen.cpp:2619-2626): the weights stay as
+  // they are on the device (the host copy may be older than them)
   m->moe_active[(size_t)k] = 0;
   m->moe_count--;
-  device_sync_weights(m);
+  upload_mask(m);
   return m->moe_count;
 }
 

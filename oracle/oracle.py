@@ -432,7 +432,7 @@ class Net:
                     k0 = comment_attr(i.comment, "initial") or E
                     if k0 <= 0 or k0 > E:
                         k0 = E
-                    self.moe = dict(D=D, E=E, H=H, K0=k0, g=i.operands[1])
+                    self.moe = dict(D=D, E=E, H=H, K0=k0, g=i.operands[1], e1=i.operands[2], e2=i.operands[3])
         self.fused = {f.name: fusion_groups(f) for f in self.funcs}
         self.in_cols, self.out_cols = self._geometry()
 
@@ -915,3 +915,66 @@ class Model:
         self._lr = np.float32(0.0)
         _, loss = self._run(self.net.train, f32(x).ravel(), f32(labels).ravel(), False)
         return np.float32(loss)
+
+    # -- MoE expert lifecycle: host-side blob edits (codegen.cpp:2562-2626) --
+    def _moe_views(self):
+        m = self.net.moe
+        return m, self.weight(m["g"]), self.weight(m["e1"]), self.weight(m["e2"])
+
+    def _noise(self, n):
+        # ((float)(rng() % 1001) / 1000.f - 0.5f) * 1e-2f, one draw per element
+        r = (self.rng.draws(n) % np.uint64(1001)).astype(np.float32)
+        return (r / np.float32(1000.0) - np.float32(0.5)) * np.float32(1e-2)
+
+    def expert_count(self):
+        return int(self.active.sum()) if self.active is not None else 0
+
+    def expert_birth(self, n):
+        """ns_expert_birth (codegen.cpp:2567-2595): a random live source
+        expert (rng() % cap, redrawn while dead, at most cap redraws) is copied
+        with per-element noise into the first n dead slots, gate column first,
+        then FFN-1, then FFN-2."""
+        m, g, e1, e2 = self._moe_views()
+        cap, D, H = m["E"], m["D"], m["H"]
+        if n <= 0 or self.expert_count() >= cap:
+            return self.expert_count()
+        src = int(self.rng.draws(1)[0] % np.uint64(cap))
+        tries = 0
+        while tries < cap and not self.active[src]:
+            tries += 1
+            src = int(self.rng.draws(1)[0] % np.uint64(cap))
+        gm = g.reshape(D, cap)
+        for e in range(cap):
+            if n <= 0:
+                break
+            if self.active[e]:
+                continue
+            gm[:, e] = gm[:, src] + self._noise(D)
+            e1[e * D * H:(e + 1) * D * H] = e1[src * D * H:(src + 1) * D * H] + self._noise(D * H)
+            e2[e * H * D:(e + 1) * H * D] = e2[src * H * D:(src + 1) * H * D] + self._noise(H * D)
+            self.active[e] = 1
+            n -= 1
+        return self.expert_count()
+
+    def expert_merge(self, a, b):
+        """ns_expert_merge (codegen.cpp:2597-2617): expert a becomes the
+        fp32 average 0.5f * (a + b) of both, b dies."""
+        m, g, e1, e2 = self._moe_views()
+        cap, D, H = m["E"], m["D"], m["H"]
+        if a < 0 or b < 0 or a == b or a >= cap or b >= cap or not self.active[a] or not self.active[b]:
+            return self.expert_count()
+        gm = g.reshape(D, cap)
+        half = np.float32(0.5)
+        gm[:, a] = half * (gm[:, a] + gm[:, b])
+        sa, sb = slice(a * D * H, (a + 1) * D * H), slice(b * D * H, (b + 1) * D * H)
+        e1[sa] = half * (e1[sa] + e1[sb])
+        e2[sa] = half * (e2[sa] + e2[sb])
+        self.active[b] = 0
+        return self.expert_count()
+
+    def expert_kill(self, k):
+        """ns_expert_kill (codegen.cpp:2619-2626): only the mask changes."""
+        if k < 0 or k >= self.net.moe["E"] or not self.active[k]:
+            return self.expert_count()
+        self.active[k] = 0
+        return self.expert_count()

@@ -116,6 +116,26 @@ def main(names=()):
             rec["life_counts"] = np.array(counts, dtype=np.int64)
             rec["life_outs"] = np.stack(outs)
             rec["life_w"] = lib.get_weights(m)
+            # the reference's NSM2 file after the lifecycle (codegen.cpp:2505-2528):
+            # digest of every byte, and the MoE tail after the blob
+            import tempfile
+            with tempfile.TemporaryDirectory() as d:
+                path = os.path.join(d, "life.nsm")
+                assert lib.save(m, path) == 0
+                with open(path, "rb") as f:
+                    raw = f.read()
+                rec["ckpt_digest"] = np.array(hashlib.sha256(raw).hexdigest())
+                rec["ckpt_tail"] = np.frombuffer(raw[12 + 4 * rec["life_w"].size:], dtype=np.uint8).copy()
+                # an NSM1 file of the initial weights loads with every slot alive
+                # (codegen.cpp:2549-2551); the forward after that load
+                nsm1 = os.path.join(d, "w.nsm1")
+                with open(nsm1, "wb") as f:
+                    f.write(np.uint32(0x4E534D31).tobytes() + np.uint64(w.size).tobytes() + w.tobytes())
+                m1 = lib.init(w)
+                assert lib.load(m1, nsm1) == 0
+                rec["nsm1_count"] = np.int64(lib.lib.ns_expert_count(m1))
+                rec["nsm1_out"] = lib.eval_infer(m1, x)[: out.size]
+                lib.free(m1)
         lib.free(m)
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **rec)
         print(name, {k: getattr(v, "shape", None) for k, v in rec.items()})

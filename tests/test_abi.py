@@ -79,3 +79,17 @@ def test_reference_build_drivers_load_when_present():
     if not os.path.exists(ref):
         pytest.skip("reference build not present")
     assert NsLib(ref).weight_count_static() == 64 * 256 + 256 * 256 + 256 * 10
+
+
+@pytest.mark.parametrize("name", ["c4k", "moet", "c4"])
+def test_moe_plan_without_initial_experts_is_rejected(name):
+    """The reference's own `nsc --mlir` printer drops MoE(initial_experts)
+    (mlir_compiler.cpp:896-902); a plan without `initial=` would not know which
+    experts start live, so it is refused instead of assuming all of them."""
+    import re
+    text = helpers.ir_text(name)
+    plain = re.sub(r" initial=\d+", "", text)
+    assert plain != text
+    with pytest.raises(runtime.NshipError, match="initial"):
+        runtime.Plan(plain)
+    runtime.Plan(text)  # the attribute-preserving text parses

@@ -76,7 +76,7 @@ def test_moe_routing_is_bit_exact(M, D, E, H, mask):
           f"  ns.tensor.alloc %moe_e1_w : Tensor[{E}, {D * H}] float32\n"
           f"  ns.tensor.alloc %moe_e2_w : Tensor[{E}, {H * D}] float32\n"
           f"  ns.layer.moe %moe0 %x %moe_g_w %moe_e1_w %moe_e2_w : Tensor[Dynamic, {D}] float32 "
-          f"// moe(x, experts={E}, {'initial=%d, ' % (E // 2) if mask else ''}ffn={H})\n"
+          f"// moe(x, experts={E}, ffn={H}) initial={E // 2 if mask else E}\n"
           "  ns.return %moe0\n}\n")
     plan = runtime.Plan(ir)
     from neuralscript_amd import synth
@@ -135,3 +135,111 @@ def test_c4_full_size():
     ref, _, _ = oracle.moe_fwd(x.reshape(M, D)[rows].ravel(), Wg, w[D * E: D * E + E * D * H],
                                w[D * E + E * D * H:], None, len(rows), D, H, E)
     helpers.assert_close(out[rows], ref.reshape(len(rows), D), "c4 rows")
+
+
+def test_lifecycle_after_training_keeps_trained_weights():
+    """Kill / merge / birth after device training act on the trained weights.
+
+    Kill only flips the liveness mask (codegen.cpp:2619-2626): the trained
+    weights read back before and after it are identical, and the forward
+    afterwards equals the oracle's with those weights and that mask.  Merge
+    and birth edit the trained blob (the host copy is refreshed from the
+    device first), so their results equal the same edits replayed by the
+    oracle's restatement on the trained weights."""
+    name, rows, seed = "moet", 41, 109
+    net, x, y = case_inputs(name, rows, seed)
+    lib = runtime.net_lib(name)
+    m = lib.init(helpers.net_weights(name, seed))
+    for _ in range(3):
+        lib.train_step(m, x, y, 0.01)
+    w_trained = lib.get_weights(m)
+    om = oracle.Model(net, w_trained)
+    live = np.flatnonzero(om.active)
+    assert len(live) >= 3
+    k = int(live[-1])
+    assert lib.lib.ns_expert_kill(m, k) == len(live) - 1
+    assert helpers.bitwise_equal(lib.get_weights(m), w_trained), "kill changed the trained weights"
+    om.active[k] = 0
+    helpers.assert_close(lib.eval_infer(m, x), om.eval_infer(x), "forward after kill")
+    # merge: averages expert a and b into a (host-side edit of the trained blob)
+    a, b = int(live[0]), int(live[1])
+    assert lib.lib.ns_expert_merge(m, a, b) == len(live) - 2
+    om.expert_merge(a, b)
+    assert helpers.bitwise_equal(lib.get_weights(m), om.w), "merge did not act on the trained weights"
+    helpers.assert_close(lib.eval_infer(m, x), om.eval_infer(x), "forward after merge")
+    # birth: a live expert (drawn from the model's mt19937) copied with noise
+    # into the first dead slot
+    assert lib.lib.ns_expert_birth(m, 1) == om.expert_birth(1) == len(live) - 1
+    assert helpers.bitwise_equal(lib.get_weights(m), om.w), "birth did not act on the trained weights"
+    helpers.assert_close(lib.eval_infer(m, x), om.eval_infer(x), "forward after birth")
+    # training continues from the edited state
+    l_dev = lib.train_step(m, x, y, 0.01)
+    l_ref = om.train_step(x, y, 0.01)
+    assert abs(l_dev - l_ref) <= 1e-5 + 1e-4 * abs(l_ref), (l_dev, l_ref)
+    lib.free(m)
+
+
+def test_moe_checkpoint_tail_matches_reference(tmp_path):
+    """NSM2 with the MoE tail (codegen.cpp:2501-2557) on c4k after birth,
+    merge and kill: the saved file is byte-identical to the reference
+    driver's; loading it restores weights and liveness; an NSM1 file loads
+    with every capacity slot alive (as the reference's load does); a file
+    with a wrong layer count, capacity or a short mask returns -1 and leaves
+    the model as it was."""
+    import hashlib
+    name = "c4k"
+    case = next(c for c in CASES if c[0] == name)
+    net, x, _ = case_inputs(name, case[1], case[2])
+    w = helpers.net_weights(name, case[2])
+    g = np.load(os.path.join(helpers.GOLDEN, f"{name}.npz"))
+    n_out = g["out"].size
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    lib.lib.ns_expert_birth(m, 1)
+    lib.lib.ns_expert_merge(m, 0, 1)
+    lib.lib.ns_expert_kill(m, 2)
+    path = str(tmp_path / "life.nsm")
+    assert lib.save(m, path) == 0
+    with open(path, "rb") as f:
+        raw = f.read()
+    assert raw[12 + 4 * w.size:] == g["ckpt_tail"].tobytes()
+    assert hashlib.sha256(raw).hexdigest() == str(g["ckpt_digest"]), "checkpoint bytes differ from the reference's"
+    lib.free(m)
+
+    m2 = lib.init(w)
+    assert lib.load(m2, path) == 0
+    assert lib.lib.ns_expert_count(m2) == int(g["life_counts"][-1])
+    assert helpers.bitwise_equal(lib.get_weights(m2), g["life_w"])
+    helpers.assert_close(lib.eval_infer(m2, x)[:n_out], g["life_outs"][-1], "forward after load")
+
+    nsm1 = str(tmp_path / "w.nsm1")
+    with open(nsm1, "wb") as f:
+        f.write(np.uint32(0x4E534D31).tobytes() + np.uint64(w.size).tobytes() + w.tobytes())
+    assert lib.load(m2, nsm1) == 0
+    assert lib.lib.ns_expert_count(m2) == int(g["nsm1_count"]) == net.moe["E"]
+    assert helpers.bitwise_equal(lib.get_weights(m2), w)
+    helpers.assert_close(lib.eval_infer(m2, x)[:n_out], g["nsm1_out"], "forward after NSM1 load")
+
+    # back to the lifecycle state, then every malformed tail is rejected
+    assert lib.load(m2, path) == 0
+    before = lib.eval_infer(m2, x)[:n_out]
+    E = net.moe["E"]
+    head = raw[: 12 + 4 * w.size]
+    mask = raw[-E:]
+    bad = {"cap+1": head + np.uint32(1).tobytes() + np.uint64(E + 1).tobytes() + mask + b"\x01",
+           "cap-1": head + np.uint32(1).tobytes() + np.uint64(E - 1).tobytes() + mask[:-1],
+           "layers=2": head + np.uint32(2).tobytes() + np.uint64(E).tobytes() + mask,
+           "short mask": head + np.uint32(1).tobytes() + np.uint64(E).tobytes() + mask[:-1],
+           "no tail": head}
+    w_other = (w * np.float32(2)).astype(np.float32)
+    for label, body in bad.items():
+        # the blob in the bad file differs, so a partial load would show
+        body = body[:12] + w_other.tobytes() + body[12 + 4 * w.size:]
+        p = str(tmp_path / f"bad_{label.replace(' ', '_')}.nsm")
+        with open(p, "wb") as f:
+            f.write(body)
+        assert lib.load(m2, p) == -1, label
+        assert lib.lib.ns_expert_count(m2) == int(g["life_counts"][-1]), label
+        assert helpers.bitwise_equal(lib.get_weights(m2), g["life_w"]), label
+        assert helpers.bitwise_equal(lib.eval_infer(m2, x)[:n_out], before), label
+    lib.free(m2)

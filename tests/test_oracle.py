@@ -299,3 +299,89 @@ def test_oracle_reproduces_reference_loss_curves(curve):
     losses = np.array([m.train_step(x, y, lr) for lr in curve_lrs(base)], dtype=np.float32)
     assert helpers.bitwise_equal(losses, g["losses"])
     assert digest(m.w) == str(g["w_final_digest"])
+
+
+# ---- pins of the row-subset and routing entry points ------------------------
+# The full-size GPU tests (c2/c3 rows, c4 routing) are checked by these
+# functions, so each is tied bitwise to an oracle function that the reference
+# fixtures pin, and the gate logits to a brute-force sequential-k sum.
+
+@pytest.mark.parametrize("M,K,N", [(37, 19, 23), (64, 64, 48), (5, 130, 7)])
+@pytest.mark.parametrize("act", range(7))
+def test_matmul_rows_equals_rows_of_matmul(M, K, N, act):
+    A = synth.normal(70 + M, M * K)
+    B = synth.normal(71 + N, K * N, 0.3)
+    full = oracle.matmul(A, B, M, K, N, act).reshape(M, N)
+    rows = np.random.default_rng(M + K).permutation(M)[: max(1, M // 2)]
+    rows = np.concatenate([rows, rows[:2], [0, M - 1]])  # repeats and both ends
+    got = oracle.matmul_rows(A, rows, B, K, N, act).reshape(len(rows), N)
+    assert helpers.bitwise_equal(got, full[rows])
+
+
+@pytest.mark.parametrize("BS,D,H", [(12, 16, 4), (33, 24, 3), (70, 32, 2)])
+def test_attention_fwd_rows_equals_rows_of_attention_fwd(BS, D, H):
+    x = synth.normal(80 + BS, BS * D)
+    W = [synth.normal(81 + BS + i, D * D, 0.3) for i in range(4)]
+    full = oracle.attention_fwd(x, *W, BS, D, H).reshape(BS, D)
+    rows = np.random.default_rng(BS).permutation(BS)[: BS // 3 + 1]
+    rows = np.concatenate([rows, [0, BS - 1, rows[0]]])
+    got = oracle.attention_fwd_rows(x, *W, rows, BS, D, H).reshape(len(rows), D)
+    assert helpers.bitwise_equal(got, full[rows])
+
+
+def _gate_logits_brute_force(x, Wg, M, D, E):
+    """lg[t,e] = sum_k x[t,k] * Wg[k,e]: one fp32 accumulator, k ascending,
+    product rounded before the add (codegen.cpp:1921-1925)."""
+    X = x.reshape(M, D)
+    G = Wg.reshape(D, E)
+    acc = np.zeros((M, E), np.float32)
+    for k in range(D):
+        acc = (acc + (X[:, k:k + 1] * G[k:k + 1, :]).astype(np.float32)).astype(np.float32)
+    return acc.ravel()
+
+
+@pytest.mark.parametrize("M,D,E,mask", [(50, 16, 8, None), (33, 40, 5, "some"), (64, 64, 64, "one")])
+def test_moe_routing_functions_agree_with_moe_fwd_and_brute_force(M, D, E, mask):
+    H = 6
+    x = synth.normal(90 + M, M * D)
+    Wg = synth.normal(91 + D, D * E, float(1 / np.sqrt(D)))
+    We1, We2 = synth.normal(92, E * D * H, 0.2), synth.normal(93, E * H * D, 0.2)
+    active = None
+    if mask == "some":
+        active = (np.arange(E) % 2 == 1).astype(np.uint8)
+    elif mask == "one":
+        active = (np.arange(E) == E - 3).astype(np.uint8)
+    lg = oracle.moe_gate_logits(x, Wg, M, D, E)
+    assert helpers.bitwise_equal(lg, _gate_logits_brute_force(x, Wg, M, D, E))
+    best, prob, lg2 = oracle.moe_route(x, Wg, active, M, D, E, want_logits=True)
+    assert helpers.bitwise_equal(lg2, lg)
+    _, fbest, fprob = oracle.moe_fwd(x, Wg, We1, We2, active, M, D, H, E)
+    assert np.array_equal(best, fbest) and helpers.bitwise_equal(prob, fprob)
+    # the choice is the first maximum of the live logits (exp is monotonic)
+    L = lg.reshape(M, E).astype(np.float64)
+    if active is not None:
+        L = np.where(active[None, :] != 0, L, -np.inf)
+    assert np.array_equal(best, L.argmax(1))
+
+
+def test_oracle_lifecycle_matches_reference_fixture():
+    """Birth / merge / kill restated on the host blob (codegen.cpp:2567-2626)
+    reproduce the reference driver's weights bit for bit (c4k fixture:
+    birth(1), merge(0, 1), kill(2))."""
+    name = "c4k"
+    case = next(c for c in CASES if c[0] == name)
+    g = load_golden(name)
+    net, x, _ = case_inputs(name, case[1], case[2])
+    m = oracle.Model(net, helpers.net_weights(name, case[2]))
+    assert m.expert_count() == 4
+    counts = [m.expert_birth(1)]
+    o1 = m.eval_infer(x)
+    counts += [m.expert_merge(0, 1)]
+    o2 = m.eval_infer(x)
+    counts += [m.expert_kill(2)]
+    o3 = m.eval_infer(x)
+    assert counts == list(g["life_counts"])
+    assert helpers.bitwise_equal(m.w, g["life_w"])
+    for o, ref in zip((o1, o2, o3), g["life_outs"]):
+        assert helpers.bitwise_equal(o[: ref.size], ref)
+    assert m.expert_kill(99) == counts[-1] and m.expert_merge(0, 0) == counts[-1]
