@@ -17,7 +17,10 @@ def ws(r, c):
     return DA(runtime.lib().nsh_op_muon_workspace(r, c) // 4 + 64)
 
 
-@pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192)])
+# (9000, 24) and (24, 9000): vectors longer than 8192 floats take the
+# per-column path instead of the register panels
+@pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192),
+                                 (9000, 24), (24, 9000), (8193, 40)])
 def test_orthonormalize_matches_oracle_mgs(r, c):
     """A square Gaussian matrix is ill-conditioned (cond ~ n), and MGS's Q
     moves by ~eps * cond under a change of summation order, so the square
