@@ -157,6 +157,21 @@ size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V);
 int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                           void* workspace);
 
+/* nsh_op_embedding_grad without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * sort state lives in a static device array of
+ * NSH_EMBEDDING_GRAD_NOALLOC_MAX_INTS ints (4 MiB, held by every GPU the
+ * library runs on until the process ends); sizes with 3*V + 1 + 2*n above it
+ * return -1.  The kernels are enqueued on `stream` (a hipStream_t; NULL = the
+ * null stream) and the call returns without waiting.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other
+ * threads) race and must be serialised by the caller.  Same result as
+ * nsh_op_embedding_grad, bit for bit. */
+#define NSH_EMBEDDING_GRAD_NOALLOC_MAX_INTS 1048576
+int nsh_op_embedding_grad_noalloc(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                                  void* stream);
+
 /* Attention core over one sequence of S tokens: ctx[S,D] = per-head
  * softmax(Q K^T / sqrt(D/H)) V; Q, K, V are [S, D]; lse (optional, [H, S])
  * receives each query's log2-sum-exp of the log2e-scaled scores; the core

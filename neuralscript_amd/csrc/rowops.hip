@@ -13,6 +13,8 @@
 // deterministic and bit-exact: tokens are grouped by row with a stable
 // counting sort and each output element sums its tokens in token order, as
 // the reference's sequential scatter-add does.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -521,6 +523,12 @@ __global__ __launch_bounds__(256) void emb_grad_rows_kernel(const float* __restr
   }
 }
 
+// Clears n ints.  A kernel rather than hipMemsetAsync, so that a caller may
+// capture the launch sequence in a HIP graph (memset nodes are avoided).
+__global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0;
+}
+
 // Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
 size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
 
@@ -531,8 +539,14 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
   int* cursor = ws + 2 * V + 1;
   int* order = ws + 3 * V + 1;
   int* tmp = order + n;
-  NSH_CHECK(hipMemsetAsync(count, 0, (size_t)V * sizeof(int), s));
-  NSH_CHECK(hipMemsetAsync(cursor, 0, (size_t)V * sizeof(int), s));
+  // count [0, V) and cursor [2V+1, 3V+1) start at zero; start in between is
+  // written whole by the scan, so one fill covers [0, 3V+1)
+  if (V > 0) {
+    const int64_t nz = 3 * V + 1;
+    hipLaunchKernelGGL(fill_zero_ints_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(nz, 256), 1024)), dim3(256), 0,
+                       s, ws, nz);
+    NSH_LAUNCHED();
+  }
   if (n > 0) {
     hipLaunchKernelGGL(emb_count_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, s, idx, n, V, count);
     NSH_LAUNCHED();

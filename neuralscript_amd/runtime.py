@@ -92,6 +92,7 @@ def lib():
             "nsh_op_act_grad": (ci, [vp, vp, vp, i64, ci]),
             "nsh_op_embedding_grad_workspace": (sz, [i64, i64]),
             "nsh_op_embedding_grad": (ci, [vp, vp, vp, i64, i64, i64, vp]),
+            "nsh_op_embedding_grad_noalloc": (ci, [vp, vp, vp, i64, i64, i64, vp]),
             "nsh_op_attention_fwd": (ci, [vp, vp, vp, vp, vp, i64, i64, i64]),
         }
         for name, (res, args) in sigs.items():
