@@ -1,28 +1,35 @@
 """Benchmark of the NeuralScript HIP backend on one MI355X.
 
-Default workload = BASELINE.json configs[1] (c2): ns_eval_infer forward of the
-fp32 MLP 1024->4096 GELU->4096 GELU->1024 at batch 8192, inputs already in
-HBM (nsh_eval_infer_device), synthetic data / seeded weights.  One "step" is
-one forward pass over the 8192-row batch.
+`python bench.py` runs every GPU configuration of BASELINE.json and prints ONE
+JSON line.  The headline (`value`) is config c5 -- the largest single-GPU
+workload and the metric's "train steps/s" half: device-resident
+`ns_runtime_train_step` (nsh_train_step_device) of the emb->attn->LN->MLP->CE
+transformer on one 16384-token sequence, steps/s.  c2, c3 (ns_eval_infer
+forward, tokens/s) and c4 (MoE forward, tokens/s) are nested under
+`configs`, each with the same fields.  Inputs and weights are synthetic
+(seeded SplitMix64 streams, neuralscript_amd/workloads.py) and already in HBM
+when a timed region starts.
 
-Prints ONE JSON line with the driver's contract plus
-  roofline     -- the dominant kernel (fp32-MFMA GEMM): algorithmic FLOP per
-                  launch / average launch time from HIP events recorded on the
-                  model's stream around every launch in the timed region;
-  cpu_baseline -- the reference CPU path (the driver the reference compiler
-                  emits, built from its sources into oracle/_ref) on a bounded
-                  sample of the same workload, 1 core; the oracle port when
-                  that build is absent.
---config c3 | c4 (forward) and c5 (training step) time the other configs the
-same way (device-resident inputs) and report a per-region breakdown and the
-roofline of their dominant kernel; c4 adds the realised expert histogram and
-the top-2 gate-logit ties.
+Each config carries
+  roofline     -- its dominant kernel: algorithmic FLOP per launch / average
+                  launch time, from HIP events recorded on the model's stream
+                  around every launch in the timed region; `traffic` = HBM
+                  bytes per launch measured with rocprofv3 --pmc (profiles/);
+  cpu_baseline -- the reference's CPU path in the reference's own loop nests
+                  (oracle/ns_refloop.c, gcc -O2, one thread; pinned bitwise to
+                  the reference's emitted drivers) on a bounded sample of the
+                  same workload, extrapolated to the whole call as the
+                  `sample` field states.
+--config c2|c3|c4|c5 runs one config (profiling runs); --config peak and copy
+run the attainable-peak microbenchmarks and the rocprof calibration copy.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import platform
 import sys
 import time
 
@@ -34,10 +41,7 @@ sys.path.insert(0, ROOT)
 METRIC = "ns_eval_infer tokens/s + % of fp32-MFMA/HBM roofline; train steps/s"
 MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 HBM_PEAK_GBS = 8000.0
-
-
-def c2_flops(rows):
-    return 2.0 * rows * (1024 * 4096 + 4096 * 4096 + 4096 * 1024)
+CPU_ORDER = "reference loop nests (oracle/ns_refloop.c, gcc -O2, no FMA, one thread)"
 
 
 def load_traffic(kernel):
@@ -49,46 +53,29 @@ def load_traffic(kernel):
         return json.load(f).get(kernel)
 
 
-def cpu_baseline_c2(budget_s=15.0):
-    """Reference CPU driver (nsc --cpp --runtime, g++ -O2) on a row sample."""
-    from neuralscript_amd import runtime, workloads
-    from neuralscript_amd.abi import NsLib
-    ref = os.path.join(ROOT, "oracle", "_ref", "libc2.so")
-    plan = runtime.Plan.load("c2")
-    shapes = workloads.ir_shapes(plan.ir)
-    w = workloads.weights("c2", plan.layout(), shapes)
-    if os.path.exists(ref):
-        kind = "reference"
-        lib = NsLib(ref)
-        m = lib.init(w)
-        run = lambda x: lib.eval_infer(m, x)  # noqa: E731
-        done = lambda: lib.free(m)  # noqa: E731
-    else:
-        kind = "port"
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle
-        os.environ.setdefault("OMP_NUM_THREADS", "1")
-        om = oracle.Model(oracle.Net(plan.ir), w)
-        run = om.eval_infer
-        done = lambda: None  # noqa: E731
-    x_all = workloads.inputs("c2", rows=160)
-    t0 = time.perf_counter()
-    run(x_all[:1024])                     # 1 row: calibrates the sample size
-    t1 = time.perf_counter() - t0
-    rows = int(max(1, min(160, budget_s / max(t1, 1e-3))))
-    t0 = time.perf_counter()
-    run(x_all[: rows * 1024])
-    dt = time.perf_counter() - t0
-    done()
-    return {"value": rows / dt, "unit": "tokens/s", "cores": 1, "kind": kind,
-            "sample": f"c2 forward on {rows} of the 8192 rows (same weights/inputs), "
-                      f"{dt:.1f} s, single-threaded as the reference emits it"}
+def host_info():
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu": model, "nproc": os.cpu_count(), "glibc": "-".join(platform.libc_ver())}
 
 
-# Algorithmic work per forward of the other configs (FLOP, and bytes of the
-# bandwidth-bound kernels), for the per-kernel breakdown of --config runs.
-def c3_work(M=16384, D=1024, H=16, V=32000):
-    # gemm: 4 projections; attention: QK^T + PV over all heads;
+# ---------------------------------------------------------------------------
+# algorithmic work
+# ---------------------------------------------------------------------------
+
+def c2_work(M=8192):
+    return {"gemm": 2.0 * M * (1024 * 4096 + 4096 * 4096 + 4096 * 1024)}
+
+
+def c3_work(M=16384, D=1024):
+    # gemm: the 4 projections; attention: QK^T + PV over all heads;
     # embedding / layernorm: bytes (one read + one write of [M, D] fp32)
     return {"gemm": 2.0 * M * D * D * 4, "attention_fwd": 4.0 * M * M * D,
             "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4}
@@ -98,22 +85,151 @@ def c4_work(M=65536, D=1024, E=64, H=1024):
     return {"moe_route": 2.0 * M * D * E, "moe_experts": 4.0 * M * D * H}
 
 
-# Dominant kernel of each --config run: (profile region, kernel, bound).
-DOMINANT = {"c3": ("attention_fwd", "flash_fwd_kernel<64>", "mfma"),
+def c5_work(M=16384, D=512, FF=2048, C=8192):
+    """Algorithmic FLOP of one c5 training step (attention counted once: its
+    forward QK^T + PV, its backward dV, dP, dQ, dK)."""
+    dense_fwd = 2.0 * M * (4 * D * D + D * FF + FF * D + D * C)
+    return {"dense": 3 * dense_fwd, "attention_fwd": 4.0 * M * M * D, "attention_bwd": 8.0 * M * M * D,
+            "total": 3 * dense_fwd + 12.0 * M * M * D}
+
+
+def c5_hbm_bytes(n_muon, M=16384, D=512, C=8192):
+    """Algorithmic HBM bytes per step of c5's bandwidth-bound regions: CE reads
+    the logits and the one-hot labels and writes the gradient ([M, C] each);
+    the Muon gather reads g and writes its transpose, the update reads the q
+    vectors and w and writes w (n_muon elements each); embedding and LayerNorm
+    read and write [M, D] (LayerNorm's gradient also reads x)."""
+    return {"softmax_xent": 3.0 * M * C * 4, "muon_gather": 2.0 * n_muon * 4, "muon_update": 3.0 * n_muon * 4,
+            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4}
+
+
+HBM_REGIONS = ("embedding", "layernorm", "layernorm_grad", "softmax_xent", "muon_gather", "muon_update")
+
+# Dominant kernel of each config: (profile region, kernel name, bound).
+DOMINANT = {"c2": ("gemm", "gemm_f32_kernel", "mfma"),
+            "c3": ("attention_fwd", "flash_fwd_kernel<64>", "mfma"),
             "c4": ("moe_experts", "gemm_f32_kernel (grouped by expert, gather/scatter rows)", "mfma"),
             "c5": ("attention_bwd", "flash_bwd_dkdv_kernel<64,true> + flash_bwd_dq_ds_kernel<64>", "mfma")}
+TRAFFIC_KEY = {"c2": "gemm_f32_kernel", "c3": "c3:attention_fwd", "c4": "c4:moe_experts",
+               "c5": "c5:attention_bwd"}
 
 
-def roofline_of(key, region, work, ms_per_call):
-    """Roofline object of the dominant kernel: algorithmic FLOP of one call
-    over the HIP-event time of that call (profile region on the model's
-    stream); traffic = HBM bytes per call from rocprofv3 FETCH_SIZE /
-    WRITE_SIZE (profiles/)."""
-    _, kernel, bound = DOMINANT[key]
-    achieved = work / (ms_per_call * 1e-3) / 1e12
+def _group(prof, region):
+    """Profile entries of a region: `region` itself and its variants
+    (`gemm` and `gemm_act`: the same kernel with and without the fused
+    activation epilogue)."""
+    return [k for k in prof if not k.startswith("_") and (k == region or k.startswith(region + "_"))]
+
+
+def roofline_of(key, work, prof):
+    """Roofline object of the dominant kernel: algorithmic FLOP of one launch
+    over its average HIP-event time in the timed region."""
+    region, kernel, bound = DOMINANT[key]
+    members = _group(prof, region)
+    calls = sum(prof[k]["calls"] for k in members)
+    ms = sum(prof[k]["ms"] for k in members)
+    per_launch_ms = ms / calls
+    flop = work[region] / (calls / prof["_steps"])  # work per step / launches per step
+    achieved = flop / (per_launch_ms * 1e-3) / 1e12
     return {"bound": bound, "kernel": kernel, "region": region, "achieved": achieved, "peak": MFMA_F32_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "flop_per_launch": work,
-            "avg_launch_ms": ms_per_call, "traffic": load_traffic(f"{key}:{region}")}
+            "unit": "TFLOP/s", "frac": achieved / MFMA_F32_PEAK_TFLOPS, "flop_per_launch": flop,
+            "avg_launch_ms": per_launch_ms, "launches": calls, "profile_regions": members,
+            "traffic": load_traffic(TRAFFIC_KEY[key])}
+
+
+def kernel_table(prof, steps, work, hbm):
+    """Per profile region: ms and launches per step, and the achieved rate
+    of the regions whose algorithmic work is known (a region's variants are
+    summed, e.g. gemm + gemm_act)."""
+    out = {}
+    for k, v in prof.items():
+        if k.startswith("_"):
+            continue
+        out[k] = {"ms_per_step": v["ms"] / steps, "calls_per_step": v["calls"] / steps}
+    for k, amount in list(work.items()) + list(hbm.items()):
+        members = _group(prof, k)
+        if not members:
+            continue
+        ms = sum(prof[m]["ms"] for m in members) / steps
+        e = out[k] if members == [k] else out.setdefault(k + " (all variants)", {"ms_per_step": ms})
+        if k in hbm:
+            e["GB/s"] = amount / (ms * 1e-3) / 1e9
+            e["hbm_frac"] = e["GB/s"] / HBM_PEAK_GBS
+        else:
+            e["TFLOP/s"] = amount / (ms * 1e-3) / 1e12
+    return out
+
+
+# ---------------------------------------------------------------------------
+# GPU legs (device-resident inputs)
+# ---------------------------------------------------------------------------
+
+def _setup(key):
+    from neuralscript_amd import runtime, workloads
+    if not runtime.has_gpu():
+        raise SystemExit("bench.py: no GPU visible to libnship")
+    wl = workloads.CONFIGS[key]
+    plan = runtime.Plan.load(wl.net)
+    w = workloads.weights(key, plan.layout(), workloads.ir_shapes(plan.ir))
+    return runtime, workloads, wl, plan, w
+
+
+def _timed(model, step, steps, warmup):
+    """warmup untimed calls, then `steps` timed calls with per-launch HIP
+    events on the model's stream; synchronised on both sides."""
+    for _ in range(warmup):
+        step()
+    model.sync()
+    model.profile(True)
+    model.profile_reset()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    model.sync()
+    dt = time.perf_counter() - t0
+    prof = model.profile_report()
+    model.profile(False)
+    prof["_steps"] = steps
+    return dt, prof
+
+
+def bench_forward(key, steps, warmup, with_cpu, budget):
+    """Device-resident forward (nsh_eval_infer_device) of config `key`."""
+    runtime, workloads, wl, plan, w = _setup(key)
+    x = workloads.inputs(key)
+    model = runtime.Model(plan, w)
+    dx = runtime.DeviceArray.from_host(x)
+    dy = runtime.DeviceArray(wl.rows * plan.out_cols)
+    dt, prof = _timed(model, lambda: model.eval_infer_device(dx, dy), steps, warmup)
+    out = dy.to_host()
+    if not np.isfinite(out).all():
+        raise SystemExit(f"bench.py: non-finite {key} output")
+    # host-pointer ABI (ns_eval_infer: PCIe copies included), for reference
+    model.eval_infer(x)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        model.eval_infer(x)
+    abi_dt = (time.perf_counter() - t0) / 3
+    routing = None
+    if key == "c4":
+        E = workloads.ir_shapes(plan.ir)["moe_g_w"][1]
+        best, _, lg = model.last_routing(wl.rows, E)
+        routing = routing_report(best, lg, E)
+    model.free()
+    dx.free()
+    dy.free()
+    work = {"c2": c2_work, "c3": c3_work, "c4": c4_work}[key]()
+    hbm = {k: v for k, v in work.items() if k in HBM_REGIONS}
+    res = {"value": wl.rows * steps / dt, "unit": "tokens/s", "ms_per_step": dt * 1e3 / steps,
+           "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device",
+           "roofline": roofline_of(key, work, prof), "kernels": kernel_table(prof, steps, work, hbm),
+           "host_abi": {"tokens_per_s": wl.rows / abi_dt, "ms": abi_dt * 1e3,
+                        "note": "ns_eval_infer with host buffers (PCIe-inclusive)"}}
+    if routing is not None:
+        res["routing"] = routing
+    if with_cpu:
+        res["cpu_baseline"] = {"c2": cpu_c2, "c3": cpu_c3, "c4": cpu_c4}[key](w, budget)
+    return res
 
 
 def routing_report(best, logits, E):
@@ -128,90 +244,10 @@ def routing_report(best, logits, E):
             "near_ties_1e-6": int(((gap > 0) & (gap <= 1e-6 * np.maximum(1.0, np.abs(top2[:, 1])))).sum())}
 
 
-def bench_forward(key, steps, warmup):
-    """Device-resident forward of config `key`; per-kernel HIP-event times."""
-    from neuralscript_amd import runtime, workloads
-    if not runtime.has_gpu():
-        raise SystemExit("bench.py: no GPU visible to libnship")
-    wl = workloads.CONFIGS[key]
-    plan = runtime.Plan.load(wl.net)
-    w = workloads.weights(key, plan.layout(), workloads.ir_shapes(plan.ir))
-    x = workloads.inputs(key)
-    model = runtime.Model(plan, w)
-    dx = runtime.DeviceArray.from_host(x)
-    dy = runtime.DeviceArray(wl.rows * plan.out_cols)
-    for _ in range(warmup):
-        model.eval_infer_device(dx, dy)
-    model.sync()
-    model.profile(True)
-    model.profile_reset()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        model.eval_infer_device(dx, dy)
-    model.sync()
-    dt = time.perf_counter() - t0
-    prof = model.profile_report()
-    model.profile(False)
-    # host-pointer ABI (ns_eval_infer: PCIe copies included), for reference
-    model.eval_infer(x)
-    t0 = time.perf_counter()
-    for _ in range(3):
-        model.eval_infer(x)
-    abi_dt = (time.perf_counter() - t0) / 3
-    routing = None
-    if key == "c4":
-        E = workloads.ir_shapes(plan.ir)["moe_g_w"][1]
-        best, _, lg = model.last_routing(wl.rows, E)
-        routing = routing_report(best, lg, E)
-    model.free()
-    work = {"c3": c3_work, "c4": c4_work}.get(key, lambda: {})()
-    kernels = {}
-    for k, v in prof.items():
-        ms = v["ms"] / steps
-        e = {"ms_per_step": ms, "calls_per_step": v["calls"] / steps}
-        if k in work:
-            if k in ("embedding", "layernorm"):  # work = bytes read + written
-                e["GB/s"] = work[k] / (ms * 1e-3) / 1e9
-            else:
-                e["TFLOP/s"] = work[k] / (ms * 1e-3) / 1e12
-        kernels[k] = e
-    region = DOMINANT[key][0]
-    out = {"metric": METRIC, "value": wl.rows * steps / dt, "unit": "tokens/s", "n_gpus": 1, "steps": steps,
-           "warmup": warmup, "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-           "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device"},
-           "roofline": roofline_of(key, region, work[region],
-                                   prof[region]["ms"] / prof[region]["calls"]),
-           "kernels": kernels}
-    out["host_abi"] = {"tokens_per_s": wl.rows / abi_dt, "ms": abi_dt * 1e3,
-                       "note": "ns_eval_infer with host buffers (PCIe-inclusive)"}
-    if routing is not None:
-        out["routing"] = routing
-    return out
-
-
-def c5_work(M=16384, D=512, H=8, V=8192, FF=2048, C=8192):
-    """Algorithmic FLOP of one c5 training step (attention counted once)."""
-    dense_fwd = 2.0 * M * (4 * D * D + D * FF + FF * D + D * C)
-    return {"dense": 3 * dense_fwd, "attention": 4.0 * M * M * D * 3, "attention_bwd": 8.0 * M * M * D,
-            "total": 3 * dense_fwd + 12.0 * M * M * D}
-
-
-def c5_hbm_bytes(n_muon, M=16384, D=512, C=8192):
-    """Algorithmic HBM bytes per step of c5's bandwidth-bound regions: CE reads
-    the logits and the one-hot labels and writes the gradient ([M, C] each);
-    the Muon gather reads g and writes its transpose, the update reads the q
-    vectors and w and writes w (n_muon elements each); embedding and LayerNorm
-    read and write [M, D] (LayerNorm's gradient also reads x)."""
-    return {"softmax_xent": 3.0 * M * C * 4, "muon_gather": 2.0 * n_muon * 4, "muon_update": 3.0 * n_muon * 4,
-            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4}
-
-
 def adamw_bandwidth(n, launches=20):
     """The AdamW kernel (nsh_op_adamw_step) over n parameters, as if every
     weight of the step took AdamW: 4 arrays read, 3 written (28 bytes per
     parameter), timed over `launches` back-to-back launches."""
-    import ctypes
     from neuralscript_amd import runtime
     bufs = [runtime.DeviceArray(n) for _ in range(4)]
     for b in bufs:
@@ -233,145 +269,260 @@ def adamw_bandwidth(n, launches=20):
             "note": "the whole parameter count of the step through the AdamW kernel (28 B per parameter)"}
 
 
-def bench_train(key, steps, warmup):
-    """Device-resident training steps of config `key` (nsh_train_step_device);
-    lr = 3e-4 times the cosine-warmup multiplier, as the host applies it."""
-    from neuralscript_amd import runtime, workloads
-    if not runtime.has_gpu():
-        raise SystemExit("bench.py: no GPU visible to libnship")
-    wl = workloads.CONFIGS[key]
-    plan = runtime.Plan.load(wl.net)
-    w = workloads.weights(key, plan.layout(), workloads.ir_shapes(plan.ir))
+def bench_train(key, steps, warmup, with_cpu, budget):
+    """Device-resident training steps (nsh_train_step_device); lr = 3e-4
+    times the cosine-warmup multiplier, as the host applies it."""
+    runtime, workloads, wl, plan, w = _setup(key)
     dx = runtime.DeviceArray.from_host(workloads.inputs(key))
     dy = runtime.DeviceArray.from_host(workloads.labels(key))
     model = runtime.Model(plan, w)
-    scale = lambda t: min(1.0, t / 100.0)  # noqa: E731  (warmup ramp; t < 100 here)
-    t = 0
-    for _ in range(warmup):
-        model.train_step_device(dx, dy, 3e-4 * scale(t), want_loss=False)
-        t += 1
-    model.sync()
-    model.profile(True)
-    model.profile_reset()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        model.train_step_device(dx, dy, 3e-4 * scale(t), want_loss=False)
-        t += 1
-    model.sync()
-    dt = time.perf_counter() - t0
-    prof = model.profile_report()
-    model.profile(False)
-    loss = model.train_step_device(dx, dy, 3e-4 * scale(t))
-    t += 1
+    t = [0]
+
+    def step():
+        model.train_step_device(dx, dy, 3e-4 * min(1.0, t[0] / 100.0), want_loss=False)
+        t[0] += 1
+
+    dt, prof = _timed(model, step, steps, warmup)
+    loss = model.train_step_device(dx, dy, 3e-4 * min(1.0, t[0] / 100.0))
+    t[0] += 1
     # host-pointer ABI (ns_runtime_train_step: the [M, C] one-hot labels cross
     # PCIe every call), for reference
     xh, yh = workloads.inputs(key), workloads.labels(key)
     t0 = time.perf_counter()
     for _ in range(2):
-        model.train_step(xh, yh, 3e-4 * scale(t))
-        t += 1
+        model.train_step(xh, yh, 3e-4 * min(1.0, t[0] / 100.0))
+        t[0] += 1
     abi_dt = (time.perf_counter() - t0) / 2
     model.free()
+    dx.free()
+    dy.free()
     work = c5_work()
     shapes = workloads.ir_shapes(plan.ir)
     # Muon matrices (codegen.cpp:3097): every 2-D weight with min(r, c) >= 8
     n_muon = sum(int(np.prod(v)) for v in shapes.values() if len(v) == 2 and min(v) >= 8)
-    hbm = c5_hbm_bytes(n_muon)
-    kernels = {}
-    for k, v in prof.items():
-        ms = v["ms"] / steps
-        e = {"ms_per_step": ms, "calls_per_step": v["calls"] / steps}
-        if k in hbm:
-            e["GB/s"] = hbm[k] / (ms * 1e-3) / 1e9
-            e["hbm_frac"] = e["GB/s"] / HBM_PEAK_GBS
-        kernels[k] = e
-    att = prof["attention_bwd"]
-    return {"metric": METRIC, "value": steps / dt, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
-            "ms_per_step": dt * 1e3 / steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32", "data": "synthetic",
-            "config": {"workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device"},
-            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
-            "roofline": roofline_of(key, "attention_bwd", work["attention_bwd"], att["ms"] / att["calls"]),
-            "kernels": kernels, "adamw": adamw_bandwidth(n_muon),
-            "host_abi": {"steps_per_s": 1.0 / abi_dt, "ms": abi_dt * 1e3,
-                         "note": "ns_runtime_train_step with host buffers (labels uploaded every call)"}}
-
-
-def bench_c2(steps, warmup, with_cpu):
-    from neuralscript_amd import runtime, workloads
-    if not runtime.has_gpu():
-        raise SystemExit("bench.py: no GPU visible to libnship")
-    rows = workloads.CONFIGS["c2"].rows
-    plan = runtime.Plan.load("c2")
-    shapes = workloads.ir_shapes(plan.ir)
-    w = workloads.weights("c2", plan.layout(), shapes)
-    x = workloads.inputs("c2")
-    model = runtime.Model(plan, w)
-    dx = runtime.DeviceArray.from_host(x)
-    dy = runtime.DeviceArray(rows * 1024)
-    for _ in range(warmup):
-        model.eval_infer_device(dx, dy)
-    model.sync()
-    # timed region: K forward steps, per-launch HIP events on the model stream
-    model.profile(True)
-    model.profile_reset()
-    model.sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        model.eval_infer_device(dx, dy)
-    model.sync()
-    dt = time.perf_counter() - t0
-    prof = model.profile_report()
-    model.profile(False)
-    out = dy.to_host()
-    if not np.isfinite(out).all():
-        raise SystemExit("bench.py: non-finite output")
-    # host-pointer ABI rate (PCIe-inclusive), for reference only
-    t0 = time.perf_counter()
-    for _ in range(3):
-        model.eval_infer(x)
-    abi_dt = (time.perf_counter() - t0) / 3
-
-    gemm_calls = sum(v["calls"] for k, v in prof.items() if k.startswith("gemm"))
-    gemm_ms = sum(v["ms"] for k, v in prof.items() if k.startswith("gemm"))
-    per_launch_ms = gemm_ms / max(gemm_calls, 1)
-    flop_per_launch = c2_flops(rows) / 3.0
-    achieved = flop_per_launch / (per_launch_ms * 1e-3) / 1e12
-    res = {
-        "metric": METRIC,
-        "value": rows * steps / dt,
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": dt * 1e3 / steps,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {"workload": "c2: " + workloads.CONFIGS["c2"].desc, "batch": rows,
-                   "layers": "1024->4096->4096->1024", "entry": "nsh_eval_infer_device"},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel", "achieved": achieved,
-                     "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": achieved / MFMA_F32_PEAK_TFLOPS,
-                     "flop_per_launch": flop_per_launch, "avg_launch_ms": per_launch_ms,
-                     "launches": gemm_calls, "traffic": load_traffic("gemm_f32_kernel")},
-        "host_abi": {"tokens_per_s": rows / abi_dt, "note": "ns_eval_infer with host buffers (PCIe-inclusive)"},
-    }
-    model.free()
-    res["measured_peak"] = measured_peaks()
-    res["roofline"]["frac_of_measured_peak"] = achieved / res["measured_peak"]["mfma_f32_tflops"]
+    res = {"value": steps / dt, "unit": "steps/s", "ms_per_step": dt * 1e3 / steps,
+           "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device",
+           "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
+           "roofline": roofline_of(key, work, prof), "kernels": kernel_table(prof, steps, work, c5_hbm_bytes(n_muon)),
+           "adamw": adamw_bandwidth(n_muon),
+           "host_abi": {"steps_per_s": 1.0 / abi_dt, "ms": abi_dt * 1e3,
+                        "note": "ns_runtime_train_step with host buffers (labels uploaded every call)"}}
     if with_cpu:
-        res["cpu_baseline"] = cpu_baseline_c2()
+        res["cpu_baseline"] = cpu_c5(w, budget)
     return res
 
+
+# ---------------------------------------------------------------------------
+# CPU baselines: the reference's loop nests on a bounded sample
+# ---------------------------------------------------------------------------
+
+class _RefOrder:
+    """The oracle's kernel wrappers routed to the reference-order library for
+    the duration of a `with` block."""
+
+    def __enter__(self):
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        self.oracle = oracle
+        self.prev = oracle.use_reference_order(True)
+        return oracle
+
+    def __exit__(self, *exc):
+        self.oracle.use_reference_order(self.prev)
+
+
+def _oracle_net(key):
+    from neuralscript_amd import workloads
+    with _RefOrder() as oracle:
+        with open(os.path.join(ROOT, "neuralscript_amd", "nets", workloads.CONFIGS[key].net + ".mlir")) as f:
+            return oracle.Net(f.read())
+
+
+def _baseline(value, unit, sample, seconds, extrapolated, **extra):
+    d = {"value": value, "unit": unit, "cores": 1, "kind": "port", "order": CPU_ORDER, "sample": sample,
+         "cpu_seconds": seconds, "extrapolated": extrapolated}
+    d.update(extra)
+    return d
+
+
+def cpu_c2(w, budget=10.0):
+    """The whole forward (3 GEMMs + GELU epilogues, i-j-k) on the first rows
+    of the batch; rows are independent, so tokens/s carries over."""
+    from neuralscript_amd import workloads
+    net = _oracle_net("c2")
+    x = workloads.inputs("c2", rows=256)
+    with _RefOrder() as oracle:
+        m = oracle.Model(net, w)
+        t0 = time.perf_counter()
+        m.eval_infer(x[:1024])
+        t1 = time.perf_counter() - t0
+        rows = int(max(1, min(256, budget / t1)))
+        t0 = time.perf_counter()
+        m.eval_infer(x[: rows * 1024])
+        dt = time.perf_counter() - t0
+    return _baseline(rows / dt, "tokens/s", f"c2 forward of {rows} of the 8192 rows", dt, False)
+
+
+def cpu_c3(w, budget=10.0, p_rows=64, q_rows=16):
+    """Embedding and LayerNorm over all 16384 tokens; the four D x D
+    projections on p_rows rows and the per-head S x S loops on q_rows query
+    rows against all 16384 keys, each scaled to 16384 rows (rows are
+    independent given K and V; K, V here are the sample's projections tiled
+    over the sequence, which changes values, not work)."""
+    from neuralscript_amd import workloads
+    M, D, H, V = 16384, 1024, 16, 32000
+    net = _oracle_net("c3")
+    ids = workloads.inputs("c3")
+    W = {n: w[net.offsets[n]: net.offsets[n] + r * c] for n, r, c in net.weights}
+    names = [n for n, _, _ in net.weights]
+    t = {}
+    with _RefOrder() as oracle:
+        t0 = time.perf_counter()
+        x = oracle.embedding(W[names[0]], ids, V, D)
+        t["embedding"] = time.perf_counter() - t0
+        xs = x[: p_rows * D]
+        t0 = time.perf_counter()
+        proj = [oracle.matmul(xs, W[n], p_rows, D, D) for n in names[1:5]]
+        t["projections"] = time.perf_counter() - t0
+        Q, K, Vv = (np.ascontiguousarray(np.tile(p.reshape(p_rows, D), (M // p_rows, 1)).ravel()) for p in proj[:3])
+        ctx = np.zeros(M * D, np.float32)
+        t["core"] = oracle.lib().rl_attention_core_rows(oracle.fp(Q), oracle.fp(K), oracle.fp(Vv), oracle.fp(ctx),
+                                                        M, D, H, 0, q_rows)
+        t0 = time.perf_counter()
+        oracle.layernorm(x, D)
+        t["layernorm"] = time.perf_counter() - t0
+    total = t["embedding"] + t["projections"] * M / p_rows + t["core"] * M / q_rows + t["layernorm"]
+    return _baseline(M / total, "tokens/s",
+                     f"c3 forward: embedding and LayerNorm of all {M} tokens, projections of {p_rows} rows and the "
+                     f"attention's per-head loops for {q_rows} query rows against all {M} keys, scaled to {M} rows; "
+                     f"extrapolated call time {total:.0f} s", sum(t.values()), True,
+                     parts_s={k: round(v, 4) for k, v in t.items()})
+
+
+def cpu_c4(w, budget=10.0):
+    """The per-token MoE loop (router, top-1, expert FFN) on the first
+    tokens of the batch; tokens are independent, so tokens/s carries over
+    (the sample follows the same Zipf routing)."""
+    from neuralscript_amd import workloads
+    M, D, E, H = 65536, 1024, 64, 1024
+    x = workloads.inputs("c4", rows=512)
+    Wg, We1, We2 = w[: D * E], w[D * E: D * E + E * D * H], w[D * E + E * D * H:]
+    with _RefOrder() as oracle:
+        t0 = time.perf_counter()
+        oracle.moe_fwd(x[:D], Wg, We1, We2, None, 1, D, H, E)
+        t1 = time.perf_counter() - t0
+        n = int(max(1, min(512, budget / t1)))
+        t0 = time.perf_counter()
+        oracle.moe_fwd(x[: n * D], Wg, We1, We2, None, n, D, H, E)
+        dt = time.perf_counter() - t0
+    return _baseline(n / dt, "tokens/s", f"c4 MoE forward of {n} of the {M} tokens", dt, False)
+
+
+def cpu_c5(w, budget=20.0, m_small=64, nq=8, nk=8):
+    """One training step, extrapolated per operation to c5's 16384 tokens:
+      * a whole step of the train core at m_small tokens (full D, vocabulary,
+        classes), every operation timed: GEMMs, their gradients, CE,
+        LayerNorm, embedding and their gradients scale with the token count;
+      * the attention's S x S loops timed at the full S = 16384 on a sample
+        (forward: nq query rows of all heads; backward: one head, nq query
+        rows and nk key rows, its S x S buffers filled), scaled to all rows
+        and heads; the backward runs 5 times per step, once per output
+        (codegen.cpp:3017-3051), so its recomputation counts 5 times;
+      * Muon at full size (it does not depend on the token count), except the
+        two 8192-long matrices, taken as 4x their 2048-long twins (MGS work
+        R*C^2, same access pattern)."""
+    from neuralscript_amd import synth, workloads
+    M, D, H = 16384, 512, 8
+    net = _oracle_net("c5")
+    x = workloads.inputs("c5", rows=m_small)
+    y = workloads.labels("c5", rows=m_small)
+    r = M / m_small
+    names = ["matmul", "matmul_grad_a", "matmul_grad_w", "act", "act_grad", "layernorm", "layernorm_grad",
+             "embedding", "embedding_grad_w", "cross_entropy", "loss_grad", "attention_fwd", "attention_bwd"]
+    t, split, opt = {}, (ctypes.c_double * 8)(), {}
+    with _RefOrder() as oracle:
+        orig = {n: getattr(oracle, n) for n in names}
+
+        def wrap(n):
+            f = orig[n]
+
+            def g(*a, **k):
+                t0 = time.perf_counter()
+                out = f(*a, **k)
+                dt = time.perf_counter() - t0
+                if n.startswith("attention"):
+                    oracle.lib().rl_last_attention_split(split)
+                    t[n] = list(split)
+                else:
+                    t[n] = t.get(n, 0.0) + dt
+                return out
+            return g
+
+        def opt_step(self, o, val, record):
+            L = oracle.lib()
+            done = {}
+            for k in range(0, len(o) - 1, 2):
+                name, g = o[k], o[k + 1]
+                rr, cc = self.net.shape[name]
+                if max(rr, cc) == 8192:
+                    continue
+                gr = oracle.f32(val(g)).copy()
+                t0 = time.perf_counter()
+                L.or_muon_step(oracle.fp(self.weight(name)), oracle.fp(gr), rr, cc, ctypes.c_float(self._lr))
+                opt[name] = time.perf_counter() - t0
+                done[(rr, cc)] = opt[name]
+            for k in range(0, len(o) - 1, 2):
+                rr, cc = self.net.shape[o[k]]
+                if max(rr, cc) == 8192:
+                    opt[o[k]] = 4.0 * done[(2048, cc) if rr == 8192 else (rr, 2048)]
+
+        try:
+            for n in names:
+                setattr(oracle, n, wrap(n))
+            model = oracle.Model(net, w)
+            model._opt_step = opt_step.__get__(model)
+            t0 = time.perf_counter()
+            model.train_step(x, y, 3e-4)
+            t_small = time.perf_counter() - t0
+        finally:
+            for n in names:
+                setattr(oracle, n, orig[n])
+        # the S x S loops at S = 16384 on a sample
+        t0 = time.perf_counter()
+        L = oracle.lib()
+        Q, K, V, dP = (synth.normal(11 + i, M * D, 0.5) for i in range(4))
+        ctx = np.zeros(M * D, np.float32)
+        core_f = L.rl_attention_core_rows(oracle.fp(Q), oracle.fp(K), oracle.fp(V), oracle.fp(ctx), M, D, H, 0, nq)
+        sc = np.full(M * M, 1.0 / M, np.float32)
+        ds = np.full(M * M, 1e-6, np.float32)
+        tb = (ctypes.c_double * 2)()
+        L.rl_attention_bwd_core_sample(oracle.fp(Q), oracle.fp(K), oracle.fp(V), oracle.fp(dP), oracle.fp(sc),
+                                       oracle.fp(ds), M, D, H, nq, nk, tb)
+        del sc, ds
+        t_attn_sample = time.perf_counter() - t0
+    lin = sum(v for n, v in t.items() if not n.startswith("attention"))
+    af, ab = t["attention_fwd"], t["attention_bwd"]
+    attn_fwd = af[0] * r + core_f * M / nq
+    attn_bwd_core = H * (tb[0] * M / nq + tb[1] * M / nk)
+    attn_bwd = 5 * (ab[0] * r + attn_bwd_core) + sum(ab[2:7]) * r
+    optim = sum(opt.values())
+    total = lin * r + attn_fwd + attn_bwd + optim
+    parts = {"token_linear_ops": lin * r, "attention_fwd": attn_fwd, "attention_bwd_x5": attn_bwd, "muon": optim}
+    return _baseline(1.0 / total, "steps/s",
+                     f"one c5 step extrapolated per operation: the train core at {m_small} tokens scaled to {M}, "
+                     f"the attention's S x S loops at S = {M} on {nq} query / {nk} key rows, Muon at full size; "
+                     f"extrapolated step time {total:.0f} s", t_small + t_attn_sample, True,
+                     parts_s={k: round(v, 1) for k, v in parts.items()})
+
+
+# ---------------------------------------------------------------------------
+# peaks and calibration
+# ---------------------------------------------------------------------------
 
 def measured_peaks():
     """Attainable peaks of this GPU, measured by libnship's microbenchmarks:
     a register-only fp32 MFMA loop (2048 workgroups x 4 waves, 4 independent
     32x32x2 chains per wave) and a float4 copy of 256 MiB each way."""
-    import ctypes
     from neuralscript_amd import runtime
     lib = runtime.lib()
     tf = ctypes.c_double()
@@ -448,30 +599,52 @@ def copy_calibration():
             "launches": 3}
 
 
+def headline(res, steps, warmup):
+    """The driver's contract fields around config c5's result."""
+    out = {"metric": METRIC, "value": res["value"], "unit": res["unit"], "n_gpus": 1, "steps": steps,
+           "warmup": warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded SplitMix64 weights and inputs)",
+           "config": {"workload": res["workload"], "tokens": res["tokens"], "entry": res["entry"]}}
+    for k in ("roofline", "cpu_baseline"):
+        if k in res:
+            out[k] = res[k]
+    out.update({k: v for k, v in res.items() if k not in out and k not in ("workload", "tokens", "entry")})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "copy", "peak"],
-                    help="c2 (default) is the metric's workload; c3/c4 (forward) and c5 (training steps) "
-                         "print per-kernel breakdowns; copy runs the rocprof counter calibration copy; peak "
-                         "measures the attainable MFMA / HBM peaks and the vendor library's fp32 GEMM")
+    ap.add_argument("--config", default="all", choices=["all", "c2", "c3", "c4", "c5", "copy", "peak"],
+                    help="all (default): c5 training steps/s as the headline, c2/c3/c4 forward nested under "
+                         "`configs`; c2..c5 alone (profiling runs); copy: the rocprof counter calibration "
+                         "copy; peak: attainable MFMA / HBM peaks and the vendor library's fp32 GEMM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of single-core CPU work per sampled baseline leg")
     a = ap.parse_args()
     if a.gpus != 1:
         raise SystemExit("bench.py: this build measures one GPU only (the path runs on one GPU; "
                          "--gpus must be 1)")
+    cpu = not a.no_cpu_baseline
     if a.config == "copy":
         res = copy_calibration()
     elif a.config == "peak":
         res = bench_peak()
-    elif a.config == "c2":
-        res = bench_c2(a.steps, a.warmup, not a.no_cpu_baseline)
     elif a.config == "c5":
-        res = bench_train(a.config, a.steps, a.warmup)
+        res = headline(bench_train("c5", a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
+    elif a.config in ("c2", "c3", "c4"):
+        res = headline(bench_forward(a.config, a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
     else:
-        res = bench_forward(a.config, a.steps, a.warmup)
+        res = headline(bench_train("c5", a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
+        res["configs"] = {}
+        for key in ("c2", "c3", "c4"):
+            print(f"bench.py: {key}", file=sys.stderr, flush=True)
+            res["configs"][key] = bench_forward(key, a.steps, a.warmup, cpu, a.cpu_budget)
+        res["measured_peak"] = measured_peaks()
+        res["host"] = host_info()
     print(json.dumps(res), flush=True)
 
 

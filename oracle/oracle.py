@@ -25,6 +25,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libns_oracle.so")
+# The same kernels in the reference's own loop nests, single-threaded, -O2
+# (ns_refloop.c): the CPU baseline, selected with use_reference_order().
+REF_LIB_PATH = os.path.join(_HERE, "libns_refloop.so")
 
 ACT_CODES = {"identity": 0, "relu": 1, "leaky_relu": 2, "sigmoid": 3, "tanh": 4,
              "swish": 5, "silu": 5, "gelu": 6}
@@ -32,7 +35,8 @@ ACT_CODES = {"identity": 0, "relu": 1, "leaky_relu": 2, "sigmoid": 3, "tanh": 4,
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
-_lib = None
+_libs = {}
+_order = "oracle"
 
 
 def build_command():
@@ -43,6 +47,27 @@ def build_command():
             "-fopenmp", "-fPIC", "-shared", src, "-o", LIB_PATH, "-lm"]
 
 
+def build_ref_command():
+    """The reference-order library, built as the reference's tests build the
+    emitted driver: -O2, baseline x86-64 (no FMA), no threads."""
+    src = os.path.join(_HERE, "ns_refloop.c")
+    return ["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", src,
+            "-o", REF_LIB_PATH, "-lm"]
+
+
+def use_reference_order(on=True):
+    """Route every kernel wrapper below (and so Model) to the reference-order
+    library (True) or back to the checker (False); returns the previous
+    setting.  Functions the reference-order library does not restate (the
+    MoE backward and routing helpers, the test-only MGS reordering) raise
+    while it is selected; the LR multiplier is host arithmetic and always
+    comes from the checker."""
+    global _order
+    prev = _order == "reference"
+    _order = "reference" if on else "oracle"
+    return prev
+
+
 def set_mgs_partials(p):
     """Test-only: sum each MGS dot product as p interleaved partial sums
     (p > 1) or as -p contiguous blocks (p < -1); 1 = the reference's order."""
@@ -50,11 +75,15 @@ def set_mgs_partials(p):
 
 
 def lib():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run __graft_entry__.build())")
-        L = ctypes.CDLL(LIB_PATH)
+    return _load(_order)
+
+
+def _load(which):
+    if which not in _libs:
+        path = LIB_PATH if which == "oracle" else REF_LIB_PATH
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library missing: {path} (run __graft_entry__.build())")
+        L = ctypes.CDLL(path)
         i64, sz, ci, cf = ctypes.c_int64, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
         sig = {
             "or_act": (None, [_f32p, _f32p, sz, ci]),
@@ -85,12 +114,18 @@ def lib():
             "or_lr_scale_cosine": (cf, [i64]),
             "or_set_mgs_partials": (None, [ci]),
         }
+        if which == "reference":
+            sig["rl_last_attention_split"] = (None, [ctypes.POINTER(ctypes.c_double)])
+            sig["rl_attention_core_rows"] = (ctypes.c_double, [_f32p] * 4 + [i64] * 5)
+            sig["rl_attention_bwd_core_sample"] = (None, [_f32p] * 6 + [i64] * 5 + [ctypes.POINTER(ctypes.c_double)])
         for name, (res, args) in sig.items():
+            if not hasattr(L, name):
+                continue  # not restated in reference order: calling it raises
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        _lib = L
-    return _lib
+        _libs[which] = L
+    return _libs[which]
 
 
 def fp(a):
@@ -274,7 +309,7 @@ def use_muon(r, c):
 
 
 def lr_scale_cosine(step):
-    return float(lib().or_lr_scale_cosine(step))
+    return float(_load("oracle").or_lr_scale_cosine(step))
 
 
 # ---------------------------------------------------------------------------

@@ -25,6 +25,25 @@ def load_golden(name):
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_oracle_matches_reference_fixtures(case):
+    _check_fixture(case)
+
+
+# The reference-order library (ns_refloop.c, the CPU baseline) restates the
+# kernels of every network below except the MoE backward.
+REF_ORDER = [c for c in CASES if c[0] not in ("moet", "moeb")]
+
+
+@pytest.mark.parametrize("case", REF_ORDER, ids=[c[0] for c in REF_ORDER])
+def test_reference_order_library_matches_reference_fixtures(case):
+    prev = oracle.use_reference_order(True)
+    try:
+        assert oracle.lib()._name.endswith("libns_refloop.so")
+        _check_fixture(case)
+    finally:
+        oracle.use_reference_order(prev)
+
+
+def _check_fixture(case):
     name, rows, seed, steps, lr, life = case
     g = load_golden(name)
     net, x, y = case_inputs(name, rows, seed)
