@@ -61,41 +61,57 @@ int launch_embedding(const float* W, const float* idx, float* out, int64_t n, in
 }
 
 // ---- LayerNorm forward -----------------------------------------------------
-// Row held in registers: NV float4 per lane covers up to 256*NV columns.
-template <int NV>
+// Rows held in registers: NV float4 per lane covers up to 256*NV columns;
+// each wave normalises RW rows, all of their loads issued before the first
+// reduction (more bytes in flight per wave for short rows).
+template <int NV, int RW>
 __global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                         int64_t rows, int last) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const float* xr = x + r * last;
-  float4 v[NV];
-  float sum = 0.f;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RW;
+  if (r0 >= rows) return;
+  float4 v[RW][NV];
+  float sum[RW];
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const int c = (lane + 64 * i) * 4;
-    v[i] = c < last ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-  }
-  const float mean = wave_sum(sum) / (float)last;
-  float sq = 0.f;
+  for (int q = 0; q < RW; q++) {
+    const float* xr = x + (r0 + q) * last;
+    const bool ok = r0 + q < rows;
+    sum[q] = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const int c = (lane + 64 * i) * 4;
-    if (c < last) {
-      const float a = v[i].x - mean, b = v[i].y - mean, d = v[i].z - mean, e = v[i].w - mean;
-      sq += (a * a + b * b) + (d * d + e * e);
+    for (int i = 0; i < NV; i++) {
+      const int c = (lane + 64 * i) * 4;
+      v[q][i] = ok && c < last ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  const float var = wave_sum(sq) / (float)last;
-  const float inv = 1.f / sqrtf(var + 1e-5f);
-  float* yr = y + r * last;
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const int c = (lane + 64 * i) * 4;
-    if (c < last)
-      *reinterpret_cast<float4*>(yr + c) =
-          make_float4((v[i].x - mean) * inv, (v[i].y - mean) * inv, (v[i].z - mean) * inv, (v[i].w - mean) * inv);
+  for (int q = 0; q < RW; q++) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) sum[q] += (v[q][i].x + v[q][i].y) + (v[q][i].z + v[q][i].w);
+    sum[q] = wave_sum(sum[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < RW; q++) {
+    if (r0 + q >= rows) break;
+    const float mean = sum[q] / (float)last;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c = (lane + 64 * i) * 4;
+      if (c < last) {
+        const float a = v[q][i].x - mean, b = v[q][i].y - mean, d = v[q][i].z - mean, e = v[q][i].w - mean;
+        sq += (a * a + b * b) + (d * d + e * e);
+      }
+    }
+    const float var = wave_sum(sq) / (float)last;
+    const float inv = 1.f / sqrtf(var + 1e-5f);
+    float* yr = y + (r0 + q) * last;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c = (lane + 64 * i) * 4;
+      if (c < last)
+        *reinterpret_cast<float4*>(yr + c) = make_float4((v[q][i].x - mean) * inv, (v[q][i].y - mean) * inv,
+                                                         (v[q][i].z - mean) * inv, (v[q][i].w - mean) * inv);
+    }
   }
 }
 
@@ -119,12 +135,13 @@ __global__ __launch_bounds__(256) void layernorm_any_kernel(const float* __restr
 int launch_layernorm(const float* x, float* y, int64_t rows, int64_t last, hipStream_t s) {
   if (rows <= 0) return 0;
   const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
+  const dim3 grid2((unsigned)ceil_div(rows, 8));
   const bool vec = last % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0;
   const int L = (int)last;
-  if (vec && last <= 256) hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, s, x, y, rows, L);
-  else if (vec && last <= 512) hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, s, x, y, rows, L);
-  else if (vec && last <= 1024) hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, s, x, y, rows, L);
-  else if (vec && last <= 2048) hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, s, x, y, rows, L);
+  if (vec && last <= 256) hipLaunchKernelGGL((layernorm_kernel<1, 2>), grid2, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 512) hipLaunchKernelGGL((layernorm_kernel<2, 2>), grid2, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 1024) hipLaunchKernelGGL((layernorm_kernel<4, 1>), grid, block, 0, s, x, y, rows, L);
+  else if (vec && last <= 2048) hipLaunchKernelGGL((layernorm_kernel<8, 1>), grid, block, 0, s, x, y, rows, L);
   else hipLaunchKernelGGL(layernorm_any_kernel, grid, block, 0, s, x, y, rows, L);
   NSH_LAUNCHED();
   return 0;
