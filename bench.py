@@ -114,11 +114,14 @@ TRAFFIC_KEY = {"c2": "gemm_f32_kernel", "c3": "c3:attention_fwd", "c4": "c4:moe_
                "c5": "c5:attention_bwd"}
 
 
+# Profile regions that are variants of one kernel: `gemm_act` is the GEMM
+# with the fused activation epilogue.
+REGION_VARIANTS = {"gemm": ("gemm", "gemm_act")}
+
+
 def _group(prof, region):
-    """Profile entries of a region: `region` itself and its variants
-    (`gemm` and `gemm_act`: the same kernel with and without the fused
-    activation epilogue)."""
-    return [k for k in prof if not k.startswith("_") and (k == region or k.startswith(region + "_"))]
+    """Profile entries of a region: `region` itself and its variants."""
+    return [k for k in REGION_VARIANTS.get(region, (region,)) if k in prof]
 
 
 def roofline_of(key, work, prof):
@@ -312,6 +315,35 @@ def bench_train(key, steps, warmup, with_cpu, budget):
     return res
 
 
+def bench_moe_backward(steps, warmup):
+    """The MoE backward at config 4's expert shape (d_model 1024, 64 experts,
+    FFN 1024) over 4096 Zipf-routed tokens: training steps of the `moep`
+    network (embedding -> MoE -> fc -> CE; not a BASELINE config), lr 0, with
+    the backward's phases timed as profile regions: the expert-grouped
+    products (dpre2 = dout We2[e]^T, dx += dH We1[e]^T: 4 M D H FLOP) and the
+    K-grouped weight gradients (dWe1, dWe2: 4 M D H FLOP)."""
+    from neuralscript_amd import runtime, workloads
+    M, D, H = 4096, 1024, 1024
+    plan = runtime.Plan.load("moep")
+    w, x, y = workloads.moe_training_workload(M)
+    model = runtime.Model(plan, w)
+    dx, dy = runtime.DeviceArray.from_host(x), runtime.DeviceArray.from_host(y)
+    dt, prof = _timed(model, lambda: model.train_step_device(dx, dy, 0.0, want_loss=False), steps, warmup)
+    model.free()
+    dx.free()
+    dy.free()
+    work = {"moe_bwd_grouped": 4.0 * M * D * H, "moe_bwd_kgrouped": 4.0 * M * D * H}
+    out = {"workload": "MoE backward at config 4's expert shape: moep (emb 8192x1024 -> MoE D 1024, E 64, "
+                       "FFN 1024 -> fc 16), 4096 Zipf-routed tokens, train step at lr 0",
+           "kernels": kernel_table(prof, steps, work, {})}
+    for region, flop in work.items():
+        ms = prof[region]["ms"] / prof[region]["calls"]
+        tf = flop / (ms * 1e-3) / 1e12
+        out[region] = {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                       "frac": tf / MFMA_F32_PEAK_TFLOPS, "flop_per_launch": flop, "avg_launch_ms": ms}
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baselines: the reference's loop nests on a bounded sample
 # ---------------------------------------------------------------------------
@@ -458,7 +490,7 @@ def cpu_c5(w, budget=20.0, m_small=64, nq=8, nk=8):
                 return out
             return g
 
-        def opt_step(self, o, val, record):
+        def opt_step(self, o, val, record, adamw_only=False):
             L = oracle.lib()
             done = {}
             for k in range(0, len(o) - 1, 2):
@@ -617,7 +649,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="all", choices=["all", "c2", "c3", "c4", "c5", "copy", "peak"],
+    ap.add_argument("--config", default="all", choices=["all", "c2", "c3", "c4", "c5", "moe_bwd", "copy", "peak"],
                     help="all (default): c5 training steps/s as the headline, c2/c3/c4 forward nested under "
                          "`configs`; c2..c5 alone (profiling runs); copy: the rocprof counter calibration "
                          "copy; peak: attainable MFMA / HBM peaks and the vendor library's fp32 GEMM")
@@ -635,6 +667,8 @@ def main():
         res = bench_peak()
     elif a.config == "c5":
         res = headline(bench_train("c5", a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
+    elif a.config == "moe_bwd":
+        res = bench_moe_backward(a.steps, a.warmup)
     elif a.config in ("c2", "c3", "c4"):
         res = headline(bench_forward(a.config, a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
     else:
@@ -643,6 +677,8 @@ def main():
         for key in ("c2", "c3", "c4"):
             print(f"bench.py: {key}", file=sys.stderr, flush=True)
             res["configs"][key] = bench_forward(key, a.steps, a.warmup, cpu, a.cpu_budget)
+        print("bench.py: MoE backward at production shape", file=sys.stderr, flush=True)
+        res["moe_backward"] = bench_moe_backward(min(a.steps, 10), min(a.warmup, 2))
         res["measured_peak"] = measured_peaks()
         res["host"] = host_info()
     print(json.dumps(res), flush=True)

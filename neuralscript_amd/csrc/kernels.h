@@ -165,8 +165,14 @@ int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, con
 int launch_moe_experts(const float* x, const float* We1, const float* We2, const MoeWork& w, float* out, int64_t M,
                        int64_t D, int64_t H, int64_t E, hipStream_t s);
 // dx / dWg / dWe1 / dWe2 (any may be null) from the forward's MoeWork (with pre).
+// Phases of the MoE backward (run in this order; a caller may issue them as
+// separate calls to time them): the expert-grouped products (dpre2 = dout
+// We2[e]^T, the per-row routing gradients, dx), the router's dWg = x^T dg,
+// and the K-grouped weight gradients dWe1, dWe2.
+constexpr int kMoeBwdGrouped = 1, kMoeBwdGate = 2, kMoeBwdKGrouped = 4, kMoeBwdAll = 7;
 int launch_moe_backward(const float* x, const float* dout, const float* Wg, const float* We1, const float* We2,
                         const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
-                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s);
+                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s,
+                        int phases = kMoeBwdAll);
 
 }  // namespace nship

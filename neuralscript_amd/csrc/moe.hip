@@ -501,9 +501,11 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
 
 int launch_moe_backward(const float* x, const float* dout, const float* Wg, const float* We1, const float* We2,
                         const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
-                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s) {
+                        float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s,
+                        int phases) {
   if (M <= 0) return 0;
   const int* nrows = w.seg + E;
+  if (phases & kMoeBwdGrouped) {
   // dpre2[pos] = dout[perm[pos]] . We2[e]^T
   GemmArgs g;
   g.A = dout; g.B = We2; g.C = b.dpre2;
@@ -537,8 +539,11 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
     h.groups = (int)E; h.seg = w.seg; h.tiles = w.tiles; h.ntiles = w.ntiles; h.sBg = D * H;
     if (launch_gemm_ex(h, false, true, 1, s) != 0) return -1;
   }
+  }
   // dWg = x^T dg
-  if (dWg && launch_gemm(x, b.dg, dWg, D, E, M, D, E, E, true, false, 0, s) != 0) return -1;
+  if ((phases & kMoeBwdGate) && dWg && launch_gemm(x, b.dg, dWg, D, E, M, D, E, E, true, false, 0, s) != 0)
+    return -1;
+  if (!(phases & kMoeBwdKGrouped)) return 0;
   // expert-sorted copies of x and dout for the K-grouped products
   const dim3 gd((unsigned)ceil_div(M * D, 256));
   hipLaunchKernelGGL(gather_rows_kernel, gd, dim3(256), 0, s, x, w.perm, nrows, b.xs, D);

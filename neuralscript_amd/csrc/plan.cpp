@@ -319,6 +319,11 @@ Plan* parse_plan(const char* text, std::string* err) {
       auto ar = arity.find(I.op);
       if (ar != arity.end() && I.in.size() < ar->second) { *err = "too few operands: " + o; return false; }
       if (I.op == Op::OptStep && I.in.size() % 2) { *err = "odd ns.opt.step operand list"; return false; }
+      if (I.op == Op::OptStep) {
+        const std::string opt = comment_str(r.comment, "optimizer");
+        if (!opt.empty() && opt != "adamw") { *err = "unknown optimizer= " + opt; return false; }
+        I.adamw_only = opt == "adamw";
+      }
       if (I.res >= 0 && r.has_type && r.dims.size() > 1) rtc(I.res) = r.dims[1];
       if (I.res >= 0) {
         if ((int)F->srows.size() <= I.res) { F->srows.resize(I.res + 1, -1); F->scols.resize(I.res + 1, -1); }

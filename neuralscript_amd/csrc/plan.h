@@ -43,6 +43,10 @@ struct Instr {
   float value = 0.f;          // Constant
   double rate = 0.0;          // Dropout: float_attr; ActGrad of a dropout: that dropout's
   bool dropout = false;       // ActGrad: the gradient of a dropout (dIn = dOut * its mask)
+  // OptStep with `optimizer=adamw` in its comment: every weight takes AdamW.
+  // A build knob of this backend, not something the reference emits (its
+  // rule is by shape, codegen.cpp:3097).
+  bool adamw_only = false;
 };
 
 struct Value {

@@ -660,7 +660,7 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
       set_error("optimizer: missing gradient for " + W.name);
       return -1;
     }
-    const bool muon = r > 1 && c > 1 && std::min(r, c) >= 8;  // codegen.cpp:3097
+    const bool muon = !I.adamw_only && r > 1 && c > 1 && std::min(r, c) >= 8;  // codegen.cpp:3097
     if (muon) {
       MuonMat mm;
       mm.w = w;
@@ -935,11 +935,18 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
               if (!w.pre || !b.dpre2 || !b.dH || !b.hp || !b.dg || !b.xs || !b.ds || !moe_dx || !moe_dwg ||
                   !moe_dwe1 || !moe_dwe2)
                 return -1;
-              Prof p(m, "moe_bwd");
-              if (launch_moe_backward(fr.ptr[I.in[1]], fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]],
-                                      fr.ptr[I.in[4]], m->d_active, w, b, moe_dx, moe_dwg, moe_dwe1, moe_dwe2, M, q.D,
-                                      q.H, q.E, s) != 0)
-                return -1;
+              // three profile regions: the expert-grouped products (dpre2 and
+              // dx), the router gradient, the K-grouped weight gradients
+              static const std::pair<const char*, int> kPhases[] = {
+                  {"moe_bwd_grouped", kMoeBwdGrouped}, {"moe_bwd_gate", kMoeBwdGate},
+                  {"moe_bwd_kgrouped", kMoeBwdKGrouped}};
+              for (const auto& ph : kPhases) {
+                Prof p(m, ph.first);
+                if (launch_moe_backward(fr.ptr[I.in[1]], fr.ptr[I.in[0]], fr.ptr[I.in[2]], fr.ptr[I.in[3]],
+                                        fr.ptr[I.in[4]], m->d_active, w, b, moe_dx, moe_dwg, moe_dwe1, moe_dwe2, M,
+                                        q.D, q.H, q.E, s, ph.second) != 0)
+                  return -1;
+              }
               moe_done = true;
             }
             switch (I.op) {

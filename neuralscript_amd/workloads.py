@@ -115,3 +115,20 @@ def ir_shapes(ir_text):
         c = int(dims[1]) if len(dims) > 1 else 1
         shapes[name] = (r, c)
     return shapes
+
+
+def moe_training_workload(tokens=4096, V=8192, D=1024, E=64, H=1024, classes=16):
+    """The `moep` network (embedding -> top-1 MoE -> fc -> CE) at config 4's
+    expert shape, for the MoE backward at production size (not a BASELINE
+    config): the embedding's last column is 1 and the router's last row holds
+    log Zipf(1.1) priors, so routing is Zipf-skewed as in config 4.  Returns
+    (weights in TENSOR_ALLOC order, token ids, one-hot labels)."""
+    emb = synth.normal(71, V * D).reshape(V, D)
+    emb[:, D - 1] = 1.0
+    Wg = synth.normal(72, D * E, float(np.sqrt(1.0 / D))).reshape(D, E)
+    Wg[D - 1, :] = np.log(zipf_probs(E)).astype(np.float32)
+    w = np.concatenate([emb.ravel(), Wg.ravel(), synth.normal(73, E * D * H, 0.02), synth.normal(74, E * H * D, 0.02),
+                        synth.normal(75, D * classes, 0.05)])
+    x = synth.token_ids(synth.stream_seed(76, "x"), tokens, V)
+    y = synth.one_hot(synth.token_ids(synth.stream_seed(77, "y"), tokens, classes), classes)
+    return w, x, y

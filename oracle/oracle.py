@@ -907,15 +907,17 @@ class Model:
                 if which == "x":
                     width[i.result] = m["D"]
             elif op == "ns.opt.step":
-                self._opt_step(o, val, record)
+                self._opt_step(o, val, record, comment_str(i.comment, "optimizer") == "adamw")
             else:
                 raise NotImplementedError(op)
         if record is not None:
             record["buf"] = buf
         return buf, loss
 
-    def _opt_step(self, o, val, record):
-        """codegen.cpp:3088-3124, pairs in TENSOR_ALLOC order."""
+    def _opt_step(self, o, val, record, adamw_only=False):
+        """codegen.cpp:3088-3124, pairs in TENSOR_ALLOC order.  adamw_only:
+        every weight takes AdamW (the `optimizer=adamw` build knob of this
+        backend; the reference chooses by shape)."""
         lr = self._lr
         L = lib()
         for k in range(0, len(o) - 1, 2):
@@ -923,7 +925,7 @@ class Model:
             r, c = self.net.shape[name]
             w = self.weight(name)  # view into the blob: updated in place
             gr = f32(val(g)).copy()
-            if use_muon(r, c):
+            if use_muon(r, c) and not adamw_only:
                 L.or_muon_step(fp(w), fp(gr), r, c, ctypes.c_float(lr))
             else:
                 m, v, t = self.adam.get(name, (np.zeros(r * c, np.float32),

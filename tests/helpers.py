@@ -76,3 +76,62 @@ def bitwise_equal(a, b):
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- the first Muon update at full size (tests/golden/c5_full_update.npz) ----
+# Muon's update is -lr sqrt(k) Q - 0.01 lr W with Q = MGS(gradient), k =
+# min(r, c): its Frobenius norm is lr * k up to the decay term whatever the
+# summation order (every Q vector is a unit vector), and Q's vectors on the
+# gradient's determined prefix are implementation-independent.  Q entries are
+# compared at the fixture's sampled (vector, element) positions.
+
+MUON_NORM_RTOL = 1e-3
+# Largest |Q_gpu - Q_oracle| allowed on c5's full-size first update (entries
+# of unit vectors of length 512..8192, i.e. typically 0.011..0.044) unless
+# the oracle's own Q moves more than an eighth of that under 1-ulp weight
+# noise (muon_q_tolerance).
+C5_Q_ATOL = 2e-3
+
+
+def muon_update_stats(w0, w1, lr, weights, offsets, ref):
+    """Per Muon matrix: (|W1 - W0|_F, Q at the fixture's sampled positions)
+    of the step W0 -> W1 taken at learning rate lr."""
+    out = {}
+    lr = np.float32(lr)
+    for name, r, c in weights:
+        o = offsets[name]
+        a = np.asarray(w0[o:o + r * c], np.float64)
+        b = np.asarray(w1[o:o + r * c], np.float64)
+        le = np.float64(lr) * np.sqrt(np.float32(min(r, c)))
+        q = ((a - b) - 0.01 * np.float64(lr) * a) / le
+        q = q.reshape(r, c) if r < c else q.reshape(r, c).T
+        out[name] = (float(np.linalg.norm(b - a)), q[ref[f"{name}:vi"], ref[f"{name}:ei"]])
+    return out
+
+
+def muon_q_tolerance(ref, name, q_atol):
+    """q_atol, or 8x the largest movement of the same Q entries in the
+    oracle's own step from 1-ulp-perturbed weights, whichever is larger (the
+    GPU's reductions differ from the reference's in every operation, not by
+    one ulp of the inputs; at c5's full size its deviations measure 1-6x
+    that movement)."""
+    key = f"{name}:q_ulp"
+    if key not in ref:
+        return q_atol
+    return max(q_atol, 8.0 * float(np.max(np.abs(ref[key] - ref[f"{name}:q"]))))
+
+
+def muon_update_failures(stats, ref, q_atol):
+    """Reasons the update `stats` disagrees with the oracle's (empty list:
+    agrees): the norm within MUON_NORM_RTOL, the sampled Q entries (all on
+    the determined prefix) within muon_q_tolerance."""
+    fails = []
+    for name, (norm, q) in stats.items():
+        rn = float(ref[f"{name}:norm"])
+        if not abs(norm - rn) <= MUON_NORM_RTOL * rn:
+            fails.append(f"{name}: |dW| {norm:.6g} vs {rn:.6g}")
+        d = float(np.max(np.abs(q - ref[f"{name}:q"])))
+        tol = muon_q_tolerance(ref, name, q_atol)
+        if not d <= tol:
+            fails.append(f"{name}: max |dQ| {d:.3g} > {tol:.3g} on the determined prefix")
+    return fails

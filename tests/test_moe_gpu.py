@@ -243,3 +243,60 @@ def test_moe_checkpoint_tail_matches_reference(tmp_path):
         assert helpers.bitwise_equal(lib.get_weights(m2), g["life_w"]), label
         assert helpers.bitwise_equal(lib.eval_infer(m2, x)[:n_out], before), label
     lib.free(m2)
+
+
+def test_moe_backward_at_production_shape():
+    """The four MoE gradients (codegen.cpp:1388-1579) at config 4's expert
+    shape -- d_model 1024, 64 experts, FFN 1024 -- over 4096 tokens with
+    Zipf-skewed routing (the embedding's last column is 1 and the router's
+    last row carries log Zipf(1.1) priors, as config 4 folds its gate bias):
+    every element of dx, dWg, dWe1 and dWe2 against the oracle.  One
+    training step of the `moep` network (embedding -> MoE -> fc -> CE) at
+    lr 0; the oracle skips its optimizer (only the gradients are compared).
+
+    Bar: the fp32 one with its absolute term scaled to the tensor
+    (|d| <= 1e-5 rms(ref) + 1e-4 |ref|; these gradients are ~1e-5 in size),
+    or, where the reference itself is that sensitive, 4x the movement a
+    random 1-ulp perturbation of the weights causes in the oracle (a dx
+    element is a sum over 1024 + 64 terms that can cancel)."""
+    name, M = "moep", 4096
+    ir = helpers.ir_text(name)
+    net = oracle.Net(ir)
+    D, E, H = 1024, 64, 1024
+    w, x, y = workloads.moe_training_workload(M)
+    assert w.size == net.total
+    Wg = w[8192 * D: 8192 * D + D * E]
+    print(f"moe backward D={D} E={E} H={H} tokens={M}", flush=True)
+
+    def oracle_grads(weights):
+        om = oracle.Model(net, weights)
+        om._opt_step = lambda *a, **k: None
+        rec = {}
+        om.train_step(x, y, 0.0, rec)
+        return rec["buf"]
+
+    ref_buf = oracle_grads(w)
+    rng = np.random.default_rng(5)
+    wp = (w * (1 + np.float32(2.0 ** -23) * rng.choice(np.array([-1, 1], np.float32), w.size))).astype(np.float32)
+    pert_buf = oracle_grads(wp)
+    best, _, lg = oracle.moe_route(ref_buf["emb3"], Wg, None, M, D, E, want_logits=True)
+    hist = np.bincount(best, minlength=E)
+    exact, near = tie_report(lg, E)
+    print(f"  routing: busiest expert {hist.max()} tokens, {int((hist > 0).sum())} experts used, "
+          f"rarest used {hist[hist > 0].min()}; exact ties {exact}, near ties {near}")
+    model = runtime.Model(runtime.Plan(ir), w)
+    model.train_step(x, y, 0.0)
+    bad = []
+    for ins in net.train.instrs:
+        if not ins.op.startswith("ns.grad.moe."):
+            continue
+        ref = ref_buf[ins.result]
+        got = model.read_value(ins.result, ref.size)
+        atol = 1e-5 * float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+        viol = helpers.violation(got, ref, atol=atol, rtol=1e-4)
+        floor = helpers.violation(pert_buf[ins.result], ref, atol=atol, rtol=1e-4)
+        print(f"  {ins.op:18s} n={ref.size:9d} violation x{viol:.3g} (1-ulp weight noise: x{floor:.3g})")
+        if not np.all(np.isfinite(got)) or viol > max(1.0, 4.0 * floor):
+            bad.append((ins.op, viol, floor))
+    model.free()
+    assert not bad, bad

@@ -82,7 +82,10 @@ def test_adamw_steps_are_bit_exact_given_the_gradient(n, off):
 
 
 @pytest.mark.parametrize("shapes", [[(16, 12), (24, 16), (16, 40)],
-                                    [(40, 16), (16, 16), (16, 16), (16, 16), (16, 16), (16, 24), (24, 16), (16, 12)]])
+                                    [(40, 16), (16, 16), (16, 16), (16, 16), (16, 16), (16, 24), (24, 16), (16, 12)],
+                                    # more matrices than one gather launch takes (64), ragged and float4 shapes
+                                    [(16 + i % 5, 12 + 4 * (i % 3)) if i % 2 else (12 + 4 * (i % 3), 17 + i % 4)
+                                     for i in range(70)] + [(130, 72), (72, 260)]])
 def test_muon_multi_matches_oracle(shapes):
     n = len(shapes)
     ws_ = [synth.normal(20 + i, r * c, 0.2) for i, (r, c) in enumerate(shapes)]

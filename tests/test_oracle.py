@@ -404,3 +404,36 @@ def test_oracle_lifecycle_matches_reference_fixture():
     for o, ref in zip((o1, o2, o3), g["life_outs"]):
         assert helpers.bitwise_equal(o[: ref.size], ref)
     assert m.expert_kill(99) == counts[-1] and m.expert_merge(0, 0) == counts[-1]
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(helpers.GOLDEN, "c5_full_update.npz")),
+                    reason="full-size update fixture not written")
+def test_full_size_muon_update_check_rejects_broken_optimizers():
+    """The assertion of test_c5_full_size_first_muon_update_matches_oracle
+    accepts the oracle's own update and rejects the oracle's update taken
+    with a no-op optimizer (W1 = W0) and with lr x 2 (the gradient at W0 does
+    not depend on lr, so that run's update is exactly twice this one's, up
+    to the decay term, which is computed here): both fail on every matrix
+    by the update's norm."""
+    from neuralscript_amd import workloads
+    g = load_golden("c5_full_update")
+    net = oracle.Net(helpers.ir_text("c5"))
+    layout = [(n, net.offsets[n], r * c) for n, r, c in net.weights]
+    w0 = workloads.weights("c5", layout, workloads.ir_shapes(helpers.ir_text("c5")))
+    lr = float(g["lr"])
+    own, noop, double = {}, {}, {}
+    for n, r, c in net.weights:
+        o = net.offsets[n]
+        W = w0[o:o + r * c].astype(np.float64).reshape(r, c)
+        Wv = W if r < c else W.T
+        vi, ei = g[n + ":vi"], g[n + ":ei"]
+        le = np.float64(np.float32(lr)) * np.sqrt(np.float32(min(r, c)))
+        decay = 0.01 * np.float64(np.float32(lr)) * Wv[vi, ei] / le
+        q, norm = g[n + ":q"], float(g[n + ":norm"])
+        own[n] = (norm, q)
+        noop[n] = (0.0, -decay)
+        double[n] = (2.0 * norm, 2.0 * q + decay)
+    assert not helpers.muon_update_failures(own, g, helpers.C5_Q_ATOL)
+    for broken in (noop, double):
+        fails = helpers.muon_update_failures(broken, g, helpers.C5_Q_ATOL)
+        assert {f.split(":")[0] for f in fails if "|dW|" in f} == set(own), fails
