@@ -437,3 +437,27 @@ def test_full_size_muon_update_check_rejects_broken_optimizers():
     for broken in (noop, double):
         fails = helpers.muon_update_failures(broken, g, helpers.C5_Q_ATOL)
         assert {f.split(":")[0] for f in fails if "|dW|" in f} == set(own), fails
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(helpers.GOLDEN, "c5a_full.npz")),
+                    reason="full-size AdamW fixture not written")
+def test_full_size_adamw_weight_check_separates_rounding_from_broken_steps():
+    """The sampled-weight assertion of test_c5_full_size_adamw_variant_ten_steps
+    (at least half of the samples within the fp32 bar) accepts the oracle's
+    own 10 steps from 1-ulp-perturbed weights (fixture `ulp_within`) and
+    rejects a no-op optimizer, a doubled lr and lr x 1.1 (their weights,
+    to first order W0 + k (W10 - W0) for k = 0, 2, 1.1)."""
+    from neuralscript_amd import workloads
+    g = load_golden("c5a_full")
+    net = oracle.Net(helpers.ir_text("c5a"))
+    layout = [(n, net.offsets[n], r * c) for n, r, c in net.weights]
+    w0 = workloads.weights("c5", layout, workloads.ir_shapes(helpers.ir_text("c5a")))
+    wr = g["w_sample"].astype(np.float64)
+    d = wr - w0[g["idx"]].astype(np.float64)
+
+    def within(w):
+        return float(np.mean(np.abs(w - wr) <= 1e-5 + 1e-4 * np.abs(wr)))
+
+    assert float(g["ulp_within"]) >= 0.5
+    for k in (0.0, 2.0, 1.1, 0.5):
+        assert within(wr + (k - 1.0) * d) < 0.5, k
