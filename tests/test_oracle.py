@@ -461,3 +461,25 @@ def test_full_size_adamw_weight_check_separates_rounding_from_broken_steps():
     assert float(g["ulp_within"]) >= 0.5
     for k in (0.0, 2.0, 1.1, 0.5):
         assert within(wr + (k - 1.0) * d) < 0.5, k
+
+
+def test_reference_order_attention_sampling_hook_matches_the_checker():
+    """rl_attention_core_rows (the CPU baseline's sampling hook: the
+    reference's per-head loops for a range of query rows) computes the same
+    context rows as the checker's attention forward, bit for bit (Wo = I
+    makes the output projection exact)."""
+    S, D, H, i0, i1 = 96, 32, 4, 17, 53
+    x = synth.normal(501, S * D, 1.0)
+    Wq, Wk, Wv = (synth.normal(502 + i, D * D, 0.3) for i in range(3))
+    eye = np.eye(D, dtype=np.float32).ravel()
+    ref = oracle.attention_fwd(x, Wq, Wk, Wv, eye, S, D, H).reshape(S, D)
+    Q, K, V = (oracle.matmul(x, W, S, D, D) for W in (Wq, Wk, Wv))
+    prev = oracle.use_reference_order(True)
+    try:
+        ctx = np.zeros(S * D, np.float32)
+        oracle.lib().rl_attention_core_rows(oracle.fp(Q), oracle.fp(K), oracle.fp(V), oracle.fp(ctx), S, D, H, i0, i1)
+    finally:
+        oracle.use_reference_order(prev)
+    ctx = ctx.reshape(S, D)
+    assert helpers.bitwise_equal(ctx[i0:i1], ref[i0:i1])
+    assert not np.any(ctx[:i0]) and not np.any(ctx[i1:])
