@@ -100,13 +100,12 @@ struct MuonMat {
   float* w;          // weight [r][c], updated in place
   const float* g;    // gradient [r][c]
   float* T;          // work: vectors contiguous, [C][R]; q vectors on exit
-  float* norms;      // [C] (per-column path)
+  float* red;        // sliced path (R > 8192): [2][C][slices] partial sums, mgs_red_floats(R, C); else unused
   int R, C;          // vector length, number of vectors
   int transposed;    // r < c: the vectors are the rows of g
-  int nblk;          // workgroups of this matrix in each per-column MGS launch
   float le, decay;   // lr * sqrt(min(r, c)), 0.01 * lr
 };
-int muon_blocks(int C);
+size_t mgs_red_floats(int64_t R, int64_t C);
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 // MGS of every matrix: T holds the vectors on entry, the q vectors on exit.
 int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s);

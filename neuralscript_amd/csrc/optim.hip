@@ -25,15 +25,23 @@
 // step advance together in the same launches; each workgroup spreads its
 // vectors over the 1024 threads according to its own matrix's length.  Vectors live
 // contiguously in a work buffer T[C][R] (a transpose of g when r >= c).
-// Vectors longer than kMaxPanelR take the per-column path (one launch per
-// column, every workgroup recomputing |v_j| with the same tree).
+// Vectors longer than kMaxPanelR take the sliced path: every vector is cut
+// into slices of kSliceLen elements, one workgroup per slice holds its slice
+// of every vector, and one launch per column j turns column j's per-slice
+// partial sums (written by the previous launch) into |v_j| and the dots,
+// normalises q_j, projects it out of every later vector's slice in order,
+// and writes the partial sums of column j + 1 -- one grid-wide exchange per
+// column.
 #include "common.h"
 #include "kernels.h"
 
 namespace nship {
 namespace {
 
-constexpr int kCPB = 4;  // later vectors per workgroup per step (per-column path)
+constexpr int kSliceThreads = 256;                        // sliced path: threads per workgroup
+constexpr int kSliceEPT = 8;                              // elements of a vector per thread
+constexpr int kSliceLen = kSliceThreads * kSliceEPT;      // elements per slice
+constexpr int kSliceBatch = 8;                            // later vectors per block reduction
 constexpr int kPB = 8;   // panel width (vectors per workgroup, panel path)
 constexpr int kPanelThreads = 1024;
 constexpr int kPanelWaves = kPanelThreads / 64;
@@ -172,39 +180,127 @@ __global__ __launch_bounds__(256) void muon_gather_kernel(const MuonMat* __restr
   (void)nmat;
 }
 
-__global__ __launch_bounds__(256) void mgs_step_kernel(const MuonMat* __restrict__ mats, int nmat, int j) {
-  __shared__ float red[4];
-  // locate this workgroup's matrix
+__host__ __device__ __forceinline__ int mgs_slices(int64_t R) { return (int)((R + kSliceLen - 1) / kSliceLen); }
+
+// Sum of the nsl per-slice partials at p, in a fixed order (lane-strided
+// sums, then the xor butterfly): every wave of every workgroup gets the
+// same bits.
+__device__ __forceinline__ float slice_total(const float* __restrict__ p, int nsl) {
+  const int lane = threadIdx.x & 63;
+  float a = 0.f;
+  for (int i = lane; i < nsl; i += 64) a += p[i];
+  return wave_sum(a);
+}
+
+// One column step of the sliced path over every long matrix (R >
+// kMaxPanelR); j = -1 only writes column 0's partials.  red[2][C][nsl]:
+// launch j reads buffer j & 1 and writes buffer (j + 1) & 1.  The dots use
+// the unnormalised v_j, dot_c = (v_j . v_c) / |v_j|, which equals q_j . v_c
+// up to rounding; q_j itself is v_j / |v_j| element by element, as in the
+// reference, and so is each projection v_c -= dot_c q_j.
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat* __restrict__ mats, int nmat, int j) {
+  __shared__ float red[4][kSliceBatch];
   int b = blockIdx.x, mi = 0;
-  while (mi < nmat && b >= mats[mi].nblk) {
-    b -= mats[mi].nblk;
-    mi++;
+  for (; mi < nmat; mi++) {
+    const int n = mats[mi].R > kMaxPanelR ? mgs_slices(mats[mi].R) : 0;
+    if (b < n) break;
+    b -= n;
   }
   if (mi >= nmat) return;
   const MuonMat& M = mats[mi];
-  if (j >= M.C) return;
-  const int R = M.R;
-  const float* __restrict__ vj = M.T + (int64_t)j * R;
-  float s = 0.f;
-  for (int k = threadIdx.x; k < R; k += 256) s += vj[k] * vj[k];
-  const float nrm = sqrtf(block_sum(s, red)) + 1e-30f;
-  if (b == 0 && threadIdx.x == 0) M.norms[j] = nrm;
-  const int c0 = j + 1 + b * kCPB;
-  for (int c = c0; c < c0 + kCPB && c < M.C; c++) {
-    float* __restrict__ vc = M.T + (int64_t)c * R;
-    float d = 0.f;
-    for (int k = threadIdx.x; k < R; k += 256) d += (vj[k] / nrm) * vc[k];
-    const float dot = block_sum(d, red);
-    for (int k = threadIdx.x; k < R; k += 256) vc[k] -= dot * (vj[k] / nrm);
-  }
-}
+  const int C = M.C, R = M.R, nsl = mgs_slices(R);
+  if (j >= C) return;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  gfloat* __restrict__ T = as_global(M.T);
+  const float* __restrict__ Pin = M.red + (size_t)(j & 1) * C * nsl;
+  float* __restrict__ Pout = M.red + (size_t)((j + 1) & 1) * C * nsl;
+  const bool vec = R % 4 == 0 && (reinterpret_cast<uintptr_t>(M.T) & 15) == 0;
+  const int64_t s0 = (int64_t)b * kSliceLen;
+  // element e of this thread's share of the slice
+  auto at = [&](int e) -> int64_t {
+    return vec ? s0 + 4 * (t + kSliceThreads * (e >> 2)) + (e & 3) : s0 + t + kSliceThreads * e;
+  };
+  auto load = [&](int c, float (&x)[kSliceEPT]) {
+    const gfloat* row = T + (int64_t)c * R;
+    if (vec) {
+#pragma unroll
+      for (int i = 0; i < kSliceEPT / 4; i++) {
+        const int64_t k = at(4 * i);
+        fvec4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k < R) v = *reinterpret_cast<const gfloat4*>(row + k);
+        x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kSliceEPT; e++) x[e] = at(e) < R ? row[at(e)] : 0.f;
+    }
+  };
+  auto store = [&](int c, const float (&x)[kSliceEPT]) {
+    gfloat* row = T + (int64_t)c * R;
+    if (vec) {
+#pragma unroll
+      for (int i = 0; i < kSliceEPT / 4; i++) {
+        const int64_t k = at(4 * i);
+        if (k < R) *reinterpret_cast<gfloat4*>(row + k) = fvec4{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kSliceEPT; e++)
+        if (at(e) < R) row[at(e)] = x[e];
+    }
+  };
 
-__global__ __launch_bounds__(256) void mgs_normalize_kernel(const MuonMat* __restrict__ mats, int nmat) {
-  const MuonMat& M = mats[blockIdx.y];
-  const int64_t n = (int64_t)M.R * M.C;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
-    M.T[i] = M.T[i] / M.norms[i / M.R];
-  (void)nmat;
+  float q[kSliceEPT], nrm = 1.f;
+  if (j >= 0) {
+    nrm = sqrtf(slice_total(Pin + (size_t)j * nsl, nsl)) + 1e-30f;
+    load(j, q);
+#pragma unroll
+    for (int e = 0; e < kSliceEPT; e++) q[e] /= nrm;
+    store(j, q);
+  }
+  float piv[kSliceEPT];
+  for (int c0 = j + 1; c0 < C; c0 += kSliceBatch) {
+    const int nb = min(kSliceBatch, C - c0);
+    float x[kSliceBatch][kSliceEPT], d[kSliceBatch];
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; u++) {
+      if (u < nb) {
+        load(c0 + u, x[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) x[u][e] = 0.f;
+      }
+      d[u] = j >= 0 && u < nb ? slice_total(Pin + (size_t)(c0 + u) * nsl, nsl) / nrm : 0.f;
+    }
+    if (j >= 0) {
+#pragma unroll
+      for (int u = 0; u < kSliceBatch; u++) {
+        if (u >= nb) break;
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) x[u][e] -= d[u] * q[e];
+        store(c0 + u, x[u]);
+      }
+    }
+    if (c0 == j + 1) {
+#pragma unroll
+      for (int e = 0; e < kSliceEPT; e++) piv[e] = x[0][e];
+    }
+    // partial sums of column j + 1 over this slice: v_{j+1} . v_c, c >= j + 1
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; u++) {
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < kSliceEPT; e++) a += piv[e] * x[u][e];
+      d[u] = wave_sum(a);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int u = 0; u < kSliceBatch; u++) red[w][u] = d[u];
+    }
+    __syncthreads();
+    if (t < nb) Pout[(size_t)(c0 + t) * nsl + b] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    __syncthreads();
+  }
 }
 
 // Sums NV values over the 1024 threads of a workgroup; every thread gets the
@@ -404,7 +500,7 @@ __global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat*
   const int first = jp + kPB;
   int b = blockIdx.x, mi = 0;
   for (; mi < nmat; mi++) {
-    const int nvec = mats[mi].C - first;
+    const int nvec = mats[mi].R > kMaxPanelR ? 0 : mats[mi].C - first;
     const int cnt = nvec <= 0 ? 0 : (jp < 0 ? 1 : (nvec + kPB - 1) / kPB);
     if (b < cnt) break;
     b -= cnt;
@@ -518,7 +614,9 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
   return 0;
 }
 
-int muon_blocks(int C) { return (int)ceil_div(C, kCPB) > 0 ? (int)ceil_div(C, kCPB) : 1; }
+size_t mgs_red_floats(int64_t R, int64_t C) {
+  return R > kMaxPanelR ? (size_t)(2 * C * (int64_t)mgs_slices(R)) : 0;
+}
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
   if (nmat <= 0) return 0;
@@ -531,28 +629,29 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
 
 int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s) {
   if (nmat <= 0) return 0;
-  int max_r = 0, max_c = 0, col_blocks = 0;
-  int64_t max_elems = 0;
+  // panel path for vectors up to kMaxPanelR long, sliced path beyond
+  int max_c = 0, max_c_long = 0, slices = 0;
   for (int i = 0; i < nmat; i++) {
-    max_r = std::max(max_r, h_mats[i].R);
-    max_c = std::max(max_c, h_mats[i].C);
-    col_blocks += h_mats[i].nblk;
-    max_elems = std::max(max_elems, (int64_t)h_mats[i].R * h_mats[i].C);
-  }
-  if (max_r > kMaxPanelR) {
-    for (int j = 0; j < max_c; j++) {
-      hipLaunchKernelGGL(mgs_step_kernel, dim3(col_blocks), dim3(256), 0, s, d_mats, nmat, j);
-      NSH_LAUNCHED();
+    const MuonMat& M = h_mats[i];
+    if (M.R > kMaxPanelR) {
+      if (!M.red) {
+        set_error("muon: vectors longer than " + std::to_string(kMaxPanelR) + " need the partial-sum buffer");
+        return -1;
+      }
+      max_c_long = std::max(max_c_long, M.C);
+      slices += mgs_slices(M.R);
+    } else {
+      max_c = std::max(max_c, M.C);
     }
-    const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(max_elems, 256), 2048);
-    hipLaunchKernelGGL(mgs_normalize_kernel, dim3(gx, nmat), dim3(256), 0, s, d_mats, nmat);
+  }
+  for (int j = -1; slices > 0 && j < max_c_long; j++) {
+    hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j);
     NSH_LAUNCHED();
-    return 0;
   }
   for (int jp = -kPB; jp + kPB < max_c; jp += kPB) {
     int grid = 0;
     for (int i = 0; i < nmat; i++) {
-      const int nvec = h_mats[i].C - (jp + kPB);
+      const int nvec = h_mats[i].R > kMaxPanelR ? 0 : h_mats[i].C - (jp + kPB);
       if (nvec > 0) grid += jp < 0 ? 1 : (int)ceil_div(nvec, kPB);
     }
     hipLaunchKernelGGL(mgs_panel_kernel, dim3(grid), dim3(kPanelThreads), 0, s, d_mats, nmat, jp);

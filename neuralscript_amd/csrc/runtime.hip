@@ -669,9 +669,9 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
       mm.R = (int)(r < c ? c : r);
       mm.C = (int)(r < c ? r : c);
       mm.T = scratch(m, "muonT" + std::to_string(wid), (size_t)n);
-      mm.norms = scratch(m, "muonN" + std::to_string(wid), (size_t)mm.C);
-      if (!mm.T || !mm.norms) return -1;
-      mm.nblk = muon_blocks(mm.C);
+      const size_t nred = mgs_red_floats(mm.R, mm.C);
+      mm.red = nred ? scratch(m, "muonP" + std::to_string(wid), nred) : nullptr;
+      if (!mm.T || (nred && !mm.red)) return -1;
       mm.le = lr * sqrtf((float)std::min(r, c));
       mm.decay = 0.01f * lr;
       m->muon_host.push_back(mm);
@@ -1587,8 +1587,7 @@ static int op_muon(float* w, const float* g, int64_t r, int64_t c, float le, flo
   mm.C = (int)(r < c ? r : c);
   char* base = (char*)ws;
   mm.T = (float*)(base + 256);
-  mm.norms = mm.T + r * c;
-  mm.nblk = muon_blocks(mm.C);
+  mm.red = mgs_red_floats(mm.R, mm.C) ? mm.T + r * c : nullptr;
   mm.le = le;
   mm.decay = decay;
   MuonMat* d = (MuonMat*)base;
@@ -1620,9 +1619,9 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
     mm.C = (int)(r[i] < c[i] ? r[i] : c[i]);
     mm.T = wsf;
     wsf += r[i] * c[i];
-    mm.norms = wsf;
-    wsf += mm.C;
-    mm.nblk = muon_blocks(mm.C);
+    const size_t nred = mgs_red_floats(mm.R, mm.C);
+    mm.red = nred ? wsf : nullptr;
+    wsf += nred;
     mm.le = lr * sqrtf((float)std::min(r[i], c[i]));
     mm.decay = 0.01f * lr;
     mats.push_back(mm);
@@ -1635,12 +1634,13 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
 
 size_t nsh_op_muon_multi_workspace(int n, const int64_t* r, const int64_t* c) {
   size_t b = 256 * (((size_t)n * sizeof(MuonMat) + 255) / 256);
-  for (int i = 0; i < n; i++) b += (size_t)(r[i] * c[i] + std::min(r[i], c[i])) * sizeof(float);
+  for (int i = 0; i < n; i++)
+    b += (size_t)(r[i] * c[i] + (int64_t)mgs_red_floats(std::max(r[i], c[i]), std::min(r[i], c[i]))) * sizeof(float);
   return b;
 }
 
 size_t nsh_op_muon_workspace(int64_t r, int64_t c) {
-  return 256 + (size_t)(r * c + std::min(r, c)) * sizeof(float);
+  return 256 + (size_t)(r * c + (int64_t)mgs_red_floats(std::max(r, c), std::min(r, c))) * sizeof(float);
 }
 
 int nsh_op_orthonormalize(const float* g, float* q, int64_t r, int64_t c, void* workspace) {

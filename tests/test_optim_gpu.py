@@ -17,10 +17,12 @@ def ws(r, c):
     return DA(runtime.lib().nsh_op_muon_workspace(r, c) // 4 + 64)
 
 
-# (9000, 24) and (24, 9000): vectors longer than 8192 floats take the
-# per-column path instead of the register panels
+# (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001): vectors
+# longer than 8192 floats take the sliced path (2048-float slices, one launch
+# per column) instead of the register panels; odd lengths take its scalar
+# loads, 19 vectors a ragged last batch of 3
 @pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192),
-                                 (9000, 24), (24, 9000), (8193, 40)])
+                                 (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001)])
 def test_orthonormalize_matches_oracle_mgs(r, c):
     """A square Gaussian matrix is ill-conditioned (cond ~ n), and MGS's Q
     moves by ~eps * cond under a change of summation order, so the square
@@ -85,7 +87,9 @@ def test_adamw_steps_are_bit_exact_given_the_gradient(n, off):
                                     [(40, 16), (16, 16), (16, 16), (16, 16), (16, 16), (16, 24), (24, 16), (16, 12)],
                                     # more matrices than one gather launch takes (64), ragged and float4 shapes
                                     [(16 + i % 5, 12 + 4 * (i % 3)) if i % 2 else (12 + 4 * (i % 3), 17 + i % 4)
-                                     for i in range(70)] + [(130, 72), (72, 260)]])
+                                     for i in range(70)] + [(130, 72), (72, 260)],
+                                    # long vectors (sliced path) beside register-panel matrices
+                                    [(9000, 24), (64, 24), (20, 20000), (24, 16)]])
 def test_muon_multi_matches_oracle(shapes):
     n = len(shapes)
     ws_ = [synth.normal(20 + i, r * c, 0.2) for i, (r, c) in enumerate(shapes)]
