@@ -218,51 +218,117 @@ __global__ __launch_bounds__(kBlk) void moe_rank_kernel(const int* __restrict__ 
   }
 }
 
-// moe_scan_kernel with the block counts staged in LDS (nblk * E <= 16384):
-// coalesced loads, column sums from LDS, coalesced offset stores.
+// moe_scan_kernel with the block counts staged in LDS (nblk * E <= 16384),
+// transposed to [expert][block] with an odd row pitch (conflict-free when
+// staged from and written back to the [block][expert] global layout).
+// Staging keeps 16 loads in flight per lane.  One wave per expert at a
+// time, lane l owning the run of blocks [l c, (l + 1) c): the expert's total
+// and each block's offset come from one wave scan of the 64 run sums (DPP
+// row shifts plus three lane reads: no LDS round trips), and the expert
+// prefix from one wave scan per 64 experts.
 constexpr int kScanLds = 16384;
+template <int CTRL>
+__device__ __forceinline__ int dpp_shr_int(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);  // 0 where the source is outside the row
+}
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+  v += dpp_shr_int<0x111>(v);  // row_shr:1
+  v += dpp_shr_int<0x112>(v);  // row_shr:2
+  v += dpp_shr_int<0x114>(v);  // row_shr:4
+  v += dpp_shr_int<0x118>(v);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  return v + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
 __global__ __launch_bounds__(256) void moe_scan_lds_kernel(int* __restrict__ bcount, int* __restrict__ seg,
                                                            int* __restrict__ tiles, int* __restrict__ ntiles,
                                                            int nblk, int E, int bm) {
-  __shared__ int cnt[kScanLds];
+  __shared__ int cnt[kScanLds + 256];
   __shared__ int base[257], tb[257];
-  const int t = threadIdx.x;
-  const int n = nblk * E;
-  for (int i = t; i < n; i += 256) cnt[i] = bcount[i];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int P = nblk | 1;  // odd pitch
+  constexpr int kB = 16;   // rows per batch and wave
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    for (int k0 = w; k0 < nblk; k0 += 4 * kB) {
+      int v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; j++) {
+        const int k = k0 + 4 * j;
+        v[j] = (k < nblk && e < E) ? bcount[(int64_t)k * E + e] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < kB; j++) {
+        const int k = k0 + 4 * j;
+        if (k < nblk && e < E) cnt[e * P + k] = v[j];
+      }
+    }
+  }
   __syncthreads();
-  if (t < E) {
+  // this lane's run of blocks [kb, ke)
+  const int run = (nblk + 63) / 64;
+  const int kb = min(nblk, lane * run), ke = min(nblk, kb + run);
+  for (int e = w; e < E; e += 4) {
     int c = 0;
-    for (int k = 0; k < nblk; k++) c += cnt[k * E + t];
-    base[t + 1] = c;  // total of expert t, turned into the prefix below
+    for (int k = kb; k < ke; k++) c += cnt[e * P + k];
+    const int tot = __builtin_amdgcn_readlane(wave_incl_scan(c), 63);
+    if (lane == 0) base[e + 1] = tot;  // total of expert e, turned into the prefix below
   }
   __syncthreads();
-  if (t == 0) {
-    base[0] = 0;
-    tb[0] = 0;
-    for (int e = 0; e < E; e++) {
-      const int tot = base[e + 1];
-      base[e + 1] = base[e] + tot;
-      tb[e + 1] = tb[e] + (tot + bm - 1) / bm;
+  if (w == 0) {
+    int carry = 0, tcarry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int tot = e < E ? base[e + 1] : 0, nt = (tot + bm - 1) / bm;
+      const int inc = wave_incl_scan(tot), tinc = wave_incl_scan(nt);
+      if (e < E) {
+        base[e + 1] = carry + inc;
+        tb[e + 1] = tcarry + tinc;
+      }
+      carry += __builtin_amdgcn_readlane(inc, 63);
+      tcarry += __builtin_amdgcn_readlane(tinc, 63);
     }
-    *ntiles = tb[E];
-    seg[E] = base[E];
-  }
-  __syncthreads();
-  if (t < E) {
-    seg[t] = base[t];
-    int run = base[t];
-    for (int k = 0; k < nblk; k++) {
-      const int c = cnt[k * E + t];
-      cnt[k * E + t] = run;
-      run += c;
-    }
-    for (int i = 0; i < tb[t + 1] - tb[t]; i++) {
-      tiles[2 * (tb[t] + i)] = t;
-      tiles[2 * (tb[t] + i) + 1] = i;
+    if (lane == 0) {
+      base[0] = 0;
+      tb[0] = 0;
+      *ntiles = tcarry;
+      seg[E] = carry;
     }
   }
   __syncthreads();
-  for (int i = t; i < n; i += 256) bcount[i] = cnt[i];
+  for (int e = w; e < E; e += 4) {
+    int c = 0;
+    for (int k = kb; k < ke; k++) c += cnt[e * P + k];
+    int off = base[e] + wave_incl_scan(c) - c;
+    for (int k = kb; k < ke; k++) {
+      const int v = cnt[e * P + k];
+      cnt[e * P + k] = off;
+      off += v;
+    }
+    if (lane == 0) seg[e] = base[e];
+    for (int i = lane; i < tb[e + 1] - tb[e]; i += 64) {
+      tiles[2 * (tb[e] + i)] = e;
+      tiles[2 * (tb[e] + i) + 1] = i;
+    }
+  }
+  __syncthreads();
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    for (int k0 = w; k0 < nblk; k0 += 4 * kB) {
+      int v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; j++) {
+        const int k = k0 + 4 * j;
+        v[j] = (k < nblk && e < E) ? cnt[e * P + k] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < kB; j++) {
+        const int k = k0 + 4 * j;
+        if (k < nblk && e < E) bcount[(int64_t)k * E + e] = v[j];
+      }
+    }
+  }
 }
 
 // Expert segments, per-block offsets (in place over bcount) and the
