@@ -157,7 +157,12 @@ struct MoeBwdWork {
   float* dg;       // [M, E]  router logit gradient (token order)
   float* xs;       // [M, D]  x in expert-sorted order
   float* ds;       // [M, D]  dout in expert-sorted order
+  float* splitk = nullptr;   // optional: K-chunk partials of dWg = x^T dg (moe_bwd_splitk_floats)
+  size_t splitk_floats = 0;
 };
+// Floats of MoeBwdWork::splitk that let dWg = x^T dg (K = M tokens, only
+// D x E outputs) run split over K; 0 when it would not be split.
+size_t moe_bwd_splitk_floats(int64_t M, int64_t D, int64_t E);
 size_t moe_work_ints(int64_t M, int64_t E);   // int-sized words of all int arrays
 int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
                      int64_t E, hipStream_t s);

@@ -565,6 +565,21 @@ __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0.f;
 }
 
+// dWg[D, E] = x[M, D]^T dg[M, E]
+static GemmArgs dwg_args(const float* x, const float* dg, float* dWg, int64_t M, int64_t D, int64_t E) {
+  GemmArgs g;
+  g.A = x; g.B = dg; g.C = dWg;
+  g.M = (int)D; g.N = (int)E; g.K = (int)M;
+  g.lda = D; g.ldb = E; g.ldc = E;
+  return g;
+}
+
+size_t moe_bwd_splitk_floats(int64_t M, int64_t D, int64_t E) {
+  if (M <= 0 || M > INT32_MAX) return 0;
+  const GemmArgs g = dwg_args(nullptr, nullptr, nullptr, M, D, E);
+  return gemm_split_workspace(g, 1, gemm_split_count(g, 1));
+}
+
 int launch_moe_backward(const float* x, const float* dout, const float* Wg, const float* We1, const float* We2,
                         const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
                         float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s,
@@ -606,9 +621,15 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
     if (launch_gemm_ex(h, false, true, 1, s) != 0) return -1;
   }
   }
-  // dWg = x^T dg
-  if ((phases & kMoeBwdGate) && dWg && launch_gemm(x, b.dg, dWg, D, E, M, D, E, E, true, false, 0, s) != 0)
-    return -1;
+  // dWg = x^T dg: D x E outputs (a handful of tiles) over K = M tokens, split
+  // over K when the caller brought the workspace
+  if ((phases & kMoeBwdGate) && dWg) {
+    const GemmArgs g = dwg_args(x, b.dg, dWg, M, D, E);
+    const int sp = gemm_split_count(g, 1);
+    const bool split = sp > 1 && b.splitk && gemm_split_workspace(g, 1, sp) <= b.splitk_floats;
+    if ((split ? launch_gemm_split(g, true, false, 1, sp, b.splitk, s) : launch_gemm_ex(g, true, false, 1, s)) != 0)
+      return -1;
+  }
   if (!(phases & kMoeBwdKGrouped)) return 0;
   // expert-sorted copies of x and dout for the K-grouped products
   const dim3 gd((unsigned)ceil_div(M * D, 256));

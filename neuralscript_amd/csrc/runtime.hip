@@ -928,6 +928,9 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
               b.dg = scratch(m, "moe_dg", (size_t)(M * q.E));
               b.xs = scratch(m, "moe_xs", (size_t)(M * q.D));
               b.ds = scratch(m, "moe_ds", (size_t)(M * q.D));
+              b.splitk_floats = moe_bwd_splitk_floats(M, q.D, q.E);
+              b.splitk = b.splitk_floats ? scratch(m, "moe_splitk", b.splitk_floats) : nullptr;
+              if (b.splitk_floats && !b.splitk) return -1;
               moe_dx = scratch(m, "moe_gx", (size_t)(M * q.D));
               moe_dwg = scratch(m, "moe_gwg", (size_t)(q.D * q.E));
               moe_dwe1 = scratch(m, "moe_gwe1", (size_t)(q.E * q.D * q.H));
