@@ -87,6 +87,24 @@ def test_c2_full_size_rows_match_oracle():
     assert np.isfinite(out).all()
 
 
+def test_c1_stated_workload_matches_reference_driver():
+    """Config 1 exactly as stated (batch 256, Xavier-uniform weights, U[-1,1]
+    inputs): the network driver over libnship against the reference's own
+    emitted driver's output (tests/golden/c1_workload.npz)."""
+    from golden.make_golden import digest
+    g = np.load(os.path.join(helpers.GOLDEN, "c1_workload.npz"))
+    ir = helpers.ir_text("c1")
+    plan = runtime.Plan(ir)
+    w = workloads.weights("c1", plan.layout(), workloads.ir_shapes(ir))
+    x = workloads.inputs("c1")
+    assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w_digest"]), "input generator drifted"
+    lib = runtime.net_lib("c1")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x)
+    lib.free(m)
+    helpers.assert_close(out, g["out"], "c1 at its stated workload")
+
+
 def test_checkpoint_round_trip_and_errors(tmp_path):
     name = "c2s"
     lib = runtime.net_lib(name)

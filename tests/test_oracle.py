@@ -483,3 +483,24 @@ def test_reference_order_attention_sampling_hook_matches_the_checker():
     ctx = ctx.reshape(S, D)
     assert helpers.bitwise_equal(ctx[i0:i1], ref[i0:i1])
     assert not np.any(ctx[:i0]) and not np.any(ctx[i1:])
+
+
+@pytest.mark.parametrize("ref_order", [False, True])
+def test_c1_stated_workload_matches_reference_driver(ref_order):
+    """Config 1 at its stated workload (batch 256, Xavier-uniform weights,
+    U[-1,1] inputs): the checker and the reference-loop-order restatement
+    both reproduce the reference driver's output bit for bit."""
+    from neuralscript_amd import workloads
+    g = load_golden("c1_workload")
+    ir = helpers.ir_text("c1")
+    net = oracle.Net(ir)
+    layout = [(n, net.offsets[n], r * c) for n, r, c in net.weights]
+    w = workloads.weights("c1", layout, workloads.ir_shapes(ir))
+    x = workloads.inputs("c1")
+    assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w_digest"])
+    prev = oracle.use_reference_order(ref_order)
+    try:
+        out = oracle.Model(net, w).eval_infer(x)
+    finally:
+        oracle.use_reference_order(prev)
+    assert helpers.bitwise_equal(out, g["out"])
