@@ -62,8 +62,8 @@ def core_bwd_ref(Q, K, V, dO, S, D, H):
 def test_attention_core_backward_matches_float64(S, D, H, store_ds):
     """Flash backward (head size 32/64: key-parallel dK/dV pass, then dQ
     either from the stored dS or from a query-parallel pass recomputing S and
-    dP) and the small-head kernels, vs the float64 gradient; |d| <=
-    1e-4 |ref| + 1e-5 max|ref| per output."""
+    dP) and the small-head kernels, vs the float64 gradient at the fp32 bar
+    |d| <= 1e-5 + 1e-4 |ref| (measured worst: 0.05 of it)."""
     print(f"attention backward S={S} D={D} H={H} store_ds={store_ds}", flush=True)
     Q, K, V, dO = (synth.normal(S * 20 + i, S * D, 1.0) for i in range(4))
     dQ_, dK_, dV_ = (DA(S * D) for _ in range(3))
@@ -75,8 +75,9 @@ def test_attention_core_backward_matches_float64(S, D, H, store_ds):
     runtime.op("attention_bwd", gQ, gK, gV, ctx, gdO, lse, dQ_, dK_, dV_, S, D, H, store_ds, ws)
     for name, got, ref in zip(("dQ", "dK", "dV"), (dQ_, dK_, dV_), core_bwd_ref(Q, K, V, dO, S, D, H)):
         ref = ref.ravel()
-        helpers.assert_close(got.to_host(), ref, f"attention {name} S={S} D={D} H={H} ds={store_ds}",
-                             atol=1e-5 * float(np.abs(ref).max()), rtol=1e-4)
+        print(f"  {name}: violation at the plain bar x{helpers.violation(got.to_host(), ref):.3g}, "
+              f"max|ref| {float(np.abs(ref).max()):.3g}")
+        helpers.assert_close(got.to_host(), ref, f"attention {name} S={S} D={D} H={H} ds={store_ds}")
 
 
 def test_attention_layer_matches_oracle():

@@ -24,9 +24,10 @@ def ws(r, c):
 @pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192),
                                  (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001)])
 def test_orthonormalize_matches_oracle_mgs(r, c):
-    """A square Gaussian matrix is ill-conditioned (cond ~ n), and MGS's Q
-    moves by ~eps * cond under a change of summation order, so the square
-    case is made well-conditioned by a diagonal shift."""
+    """Q within the fp32 bar (1e-5 + 1e-4 |ref|) of the oracle's.  A square
+    Gaussian matrix is ill-conditioned (cond ~ n), and MGS's Q moves by ~eps
+    * cond under a change of summation order, so the square case is made
+    well-conditioned by a diagonal shift."""
     print(f"mgs {r}x{c}", flush=True)
     g = synth.normal(r * 7 + c, r * c)
     if r == c:
@@ -40,7 +41,7 @@ def test_orthonormalize_matches_oracle_mgs(r, c):
         Q = Q.T
     orth = np.abs(Q.T @ Q - np.eye(Q.shape[1])).max()
     print(f"  max |Q^T Q - I| = {orth:.3g}, max |q - ref| = {np.abs(got - ref).max():.3g}")
-    helpers.assert_close(got, ref, f"mgs {r}x{c}", atol=1e-5, rtol=1e-3)
+    helpers.assert_close(got, ref, f"mgs {r}x{c}")
 
 
 def shifted(a, off):

@@ -56,9 +56,10 @@ def test_train_steps_match_reference_fixture(case):
     obj = lib.objective_loss(m, x, y)
     assert abs(obj - g["objective"]) <= tol[-1] + 2.0 * np.max(g["band"])
     if not np.any(g["band"]):  # no Muon matrix: weights and outputs are determined
-        helpers.assert_close(lib.get_weights(m), g["w_final"], f"{name} trained weights", atol=1e-4, rtol=1e-3)
-        helpers.assert_close(lib.eval_infer(m, x)[: g["out_after"].size], g["out_after"], f"{name} forward after",
-                             atol=1e-4, rtol=1e-3)
+        print(f"  trained weights violation x{helpers.violation(lib.get_weights(m), g['w_final']):.3g}, forward "
+              f"after x{helpers.violation(lib.eval_infer(m, x)[: g['out_after'].size], g['out_after']):.3g}")
+        helpers.assert_close(lib.get_weights(m), g["w_final"], f"{name} trained weights")
+        helpers.assert_close(lib.eval_infer(m, x)[: g["out_after"].size], g["out_after"], f"{name} forward after")
     lib.free(m)
 
 
@@ -76,8 +77,8 @@ def test_objective_does_not_mutate_weights():
 
 
 def test_adamw_training_matches_oracle_step_by_step():
-    """AdamW network (xor): after every step the weights stay within fp32
-    tolerance of the oracle's (no drift accumulation)."""
+    """AdamW network (xor): after every step the weights stay within the
+    fp32 bar (1e-5 + 1e-4 |ref|) of the oracle's (no drift accumulation)."""
     name, rows, seed = "xor", 4, 103
     net, x, y = case_inputs(name, rows, seed)
     w = helpers.net_weights(name, seed)
@@ -88,7 +89,8 @@ def test_adamw_training_matches_oracle_step_by_step():
         lg = lib.train_step(m, x, y, 0.3)
         lo = om.train_step(x, y, 0.3)
         assert abs(lg - lo) <= 1e-5 + 1e-4 * abs(lo), (step, lg, lo)
-        helpers.assert_close(lib.get_weights(m), om.w, f"xor step {step}", atol=2e-5, rtol=2e-4)
+        print(f"  xor step {step}: violation x{helpers.violation(lib.get_weights(m), om.w):.3g}")
+        helpers.assert_close(lib.get_weights(m), om.w, f"xor step {step}")
     lib.free(m)
 
 
@@ -119,9 +121,10 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     the device by IR value name) against the oracle's value of the same
     name; the weights after the optimizer last.
 
-    A value passes at |d| <= 1e-5 + 1e-3 |ref|, or within 4x the movement
-    that a random 1-ulp perturbation of the weights causes in the reference
-    itself (its conditioning).  The second bound matters only where the
+    A value passes at the north star's bar, |d| <= 1e-5 + 1e-4 |ref|, or
+    within 4x the movement that a random 1-ulp perturbation of the weights
+    causes in the reference itself, measured at the same bar (its
+    conditioning).  The second bound matters only where the
     network amplifies rounding: at 2048 tokens the attention output is an
     average over 2048 rows (rms 0.025) that LayerNorm rescales by ~40, so the
     reference's own logits move by 1.2x the first bound under 1-ulp weight
@@ -160,8 +163,8 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
             continue
         ref = rec["buf"][v]
         got = model.read_value(v, ref.size)
-        viol = helpers.violation(got, ref, atol=1e-5, rtol=1e-3)
-        floor = helpers.violation(rec_p["buf"][v], ref, atol=1e-5, rtol=1e-3)
+        viol = helpers.violation(got, ref)
+        floor = helpers.violation(rec_p["buf"][v], ref)
         print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g} (1-ulp weight noise: x{floor:.3g})")
         if viol > max(1.0, 4.0 * floor):
             bad.append((ins.op, v, viol, floor))
@@ -178,7 +181,7 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
         o = net.offsets[n_]
         w0, wg, wo = w[o:o + r * c], model.read_value(n_, r * c), om.w[o:o + r * c]
         if not oracle.use_muon(r, c):
-            v = helpers.violation(wg, wo, atol=2e-5, rtol=2e-4)
+            v = helpers.violation(wg, wo)
             print(f"  weight {n_} [{r}x{c}] AdamW violation x{v:.3g}")
             assert v <= 1, n_
             continue
