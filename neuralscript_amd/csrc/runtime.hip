@@ -635,9 +635,19 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
   return 0;
 }
 
+// Order of the Muon matrices in one step's launches: longest vectors first,
+// so that the MGS panel launches dispatch the workgroups with the most work
+// per vector before the short ones (each workgroup takes a whole CU), and
+// the short matrices fill the CUs that free up.  Each matrix's result does
+// not depend on the order.
+void order_for_mgs(std::vector<MuonMat>& mats) {
+  std::stable_sort(mats.begin(), mats.end(), [](const MuonMat& a, const MuonMat& b) { return a.R > b.R; });
+}
+
 // Muon step of several matrices: descriptors to the device, gather, MGS
 // column steps, update.
-int muon_batch(MuonMat* d, const std::vector<MuonMat>& mats, int64_t max_elems, hipStream_t s) {
+int muon_batch(MuonMat* d, std::vector<MuonMat> mats, int64_t max_elems, hipStream_t s) {
+  order_for_mgs(mats);
   const int nm = (int)mats.size();
   NSH_CHECK(hipMemcpyAsync(d, mats.data(), nm * sizeof(MuonMat), hipMemcpyHostToDevice, s));
   if (launch_muon_gather(d, nm, max_elems, s) != 0) return -1;
@@ -691,6 +701,7 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
     }
   }
   if (m->muon_host.empty()) return 0;
+  order_for_mgs(m->muon_host);
   const int nm = (int)m->muon_host.size();
   MuonMat* d = reinterpret_cast<MuonMat*>(scratch(m, "muon_desc", (nm * sizeof(MuonMat) + 3) / 4));
   if (!d) return -1;
