@@ -43,9 +43,25 @@ constexpr int kSliceEPT = 8;                              // elements of a vecto
 constexpr int kSliceLen = kSliceThreads * kSliceEPT;      // elements per slice
 constexpr int kSliceBatch = 8;                            // later vectors per block reduction
 constexpr int kPB = 8;   // panel width (vectors per workgroup, panel path)
-constexpr int kPanelThreads = 1024;
+// Panel path: 8 waves of up to 16 elements per vector a thread.  Fewer,
+// fuller waves keep the block reductions of the lead chain short: every wave
+// repeats a reduction's tail, so its cost grows with the wave count while the
+// element work per workgroup does not.
+constexpr int kPanelThreads = 512;
 constexpr int kPanelWaves = kPanelThreads / 64;
-constexpr int kMaxPanelR = 8 * kPanelThreads;
+constexpr int kMaxPanelR = 16 * kPanelThreads;
+
+// x / d for a divisor d shared by many quotients, given rd = 1 / d (one
+// correctly rounded division): q = x rd, then one correction q + (x - q d) rd
+// with fused multiply-adds (Markstein's corrected quotient, P. Markstein,
+// "IA-64 and Elementary Functions", 2000).  With x, d and the quotient normal
+// it is the correctly rounded quotient, the value of x / d, at three
+// instructions instead of a full division each; a subnormal quotient may
+// differ from it in the last place.
+__device__ __forceinline__ float div_shared(float x, float d, float rd) {
+  const float q = x * rd;
+  return __builtin_fmaf(__builtin_fmaf(-q, d, x), rd, q);
+}
 
 // One AdamW element (codegen.cpp:1617-1633), contraction off so every
 // product and sum rounds as the reference's scalar code does.
@@ -253,9 +269,10 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
   float q[kSliceEPT], nrm = 1.f;
   if (j >= 0) {
     nrm = sqrtf(slice_total(Pin + (size_t)j * nsl, nsl)) + 1e-30f;
+    const float rn = 1.f / nrm;
     load(j, q);
 #pragma unroll
-    for (int e = 0; e < kSliceEPT; e++) q[e] /= nrm;
+    for (int e = 0; e < kSliceEPT; e++) q[e] = div_shared(q[e], nrm, rn);
     store(j, q);
   }
   float piv[kSliceEPT];
@@ -303,12 +320,12 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
   }
 }
 
-// Sums NV values over the 1024 threads of a workgroup; every thread gets the
-// totals as wave-uniform values.  Each 16-lane row sums through DPP and
-// stores one partial per value (64 partials: 16 waves x 4 rows); after the
-// barrier every wave re-reduces them, G = 64 / NV lanes per value reading NV
-// partials each, a DPP tree over the G lanes, and the totals are read out of
-// fixed lanes.  The order is fixed, so every workgroup and every call sums
+// Sums NV values over the kPanelThreads threads of a workgroup; every thread
+// gets the totals as wave-uniform values.  Each 16-lane row sums through DPP
+// and stores one partial per value (P = 4 kPanelWaves partials); after the
+// barrier every wave re-reduces them, G = 64 / NV lanes per value reading
+// P / G partials each (one or none when G > P), a DPP tree over the G lanes,
+// and the totals are read out of fixed lanes.  The order is fixed, so every workgroup and every call sums
 // the same way.  `red` alternates between two buffers in consecutive calls,
 // so one barrier per call suffices: a thread reads buffer b only before it
 // reaches the barrier of the next call, and buffer b is written again only
@@ -331,8 +348,8 @@ __device__ __forceinline__ float row16_reduce_scatter8(const float (&v)[8], int 
 
 template <int NV>
 __device__ __forceinline__ void panel_sum(float (&v)[NV], float* red) {
-  static_assert(kPanelWaves * 4 == 64 && (NV == 1 || NV == 2 || NV == 4 || NV == 8), "64 partials, NV | 8");
-  constexpr int G = 64 / NV;
+  constexpr int P = 4 * kPanelWaves, G = 64 / NV, GL = G < P ? G : P;  // GL: lanes holding partials
+  static_assert(P <= 64 && 64 % P == 0 && (NV == 1 || NV == 2 || NV == 4 || NV == 8), "P | 64, NV | 8");
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i = lane & 15;
   if constexpr (NV == 8) {
@@ -351,14 +368,15 @@ __device__ __forceinline__ void panel_sum(float (&v)[NV], float* red) {
   const int k = lane / G, u = lane % G;
   float p = 0.f;
 #pragma unroll
-  for (int j = 0; j < NV; j++) p += red[(u + G * j) * NV + k];
+  for (int j = 0; j * G < P; j++)
+    if (u + G * j < P) p += red[(u + G * j) * NV + k];
   p = group8_sum(p);
-  if constexpr (G >= 16) p += dpp_mov<0x140>(p);
+  if constexpr (GL >= 16) p += dpp_mov<0x140>(p);
 #pragma unroll
   for (int kk = 0; kk < NV; kk++) {
     float t = read_lane(p, kk * G);
 #pragma unroll
-    for (int r = 1; r < G / 16; r++) t += read_lane(p, kk * G + 16 * r);
+    for (int r = 1; r < GL / 16; r++) t += read_lane(p, kk * G + 16 * r);
     v[kk] = t;
   }
 }
@@ -451,9 +469,9 @@ __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (
     for (int e = 0; e < EPT; e++) s[0] += x[jj][e] * x[jj][e];
     panel_sum<1>(s, red[par]);
     par ^= 1;
-    const float nrm = sqrtf(s[0]) + 1e-30f;
+    const float nrm = sqrtf(s[0]) + 1e-30f, rn = 1.f / nrm;
 #pragma unroll
-    for (int e = 0; e < EPT; e++) x[jj][e] /= nrm;
+    for (int e = 0; e < EPT; e++) x[jj][e] = div_shared(x[jj][e], nrm, rn);
     if (jj + 1 >= nv) break;
     float d[kPB];
 #pragma unroll
@@ -477,7 +495,8 @@ __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (
 
 // Elements per thread for a vector of length R (R <= kMaxPanelR).
 __device__ __forceinline__ int panel_ept(int R) {
-  return R <= kPanelThreads ? 1 : R <= 2 * kPanelThreads ? 2 : R <= 4 * kPanelThreads ? 4 : 8;
+  return R <= kPanelThreads ? 1 : R <= 2 * kPanelThreads ? 2 : R <= 4 * kPanelThreads ? 4
+         : R <= 8 * kPanelThreads ? 8 : 16;
 }
 
 // Runs CALL with constexpr E (elements per thread) and V (float4 rows) set
@@ -492,9 +511,13 @@ __device__ __forceinline__ int panel_ept(int R) {
         if (vec_) { constexpr int E = 4; constexpr bool V = true; CALL; }                   \
         else { constexpr int E = 4; constexpr bool V = false; CALL; }                       \
         break;                                                                               \
-      default:                                                                               \
+      case 8:                                                                                \
         if (vec_) { constexpr int E = 8; constexpr bool V = true; CALL; }                   \
         else { constexpr int E = 8; constexpr bool V = false; CALL; }                       \
+        break;                                                                               \
+      default:                                                                               \
+        if (vec_) { constexpr int E = 16; constexpr bool V = true; CALL; }                  \
+        else { constexpr int E = 16; constexpr bool V = false; CALL; }                      \
         break;                                                                               \
     }                                                                                        \
   } while (0)
