@@ -458,9 +458,11 @@ __device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R,
 
 // MGS inside a panel of nv vectors held in x that already carry every
 // earlier projection: normalise v_jj, project it out of the later vectors of
-// the panel, in order.
-template <int EPT>
-__device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (*red)[64 * kPB], int& par) {
+// the panel, in order.  Each q vector is stored (to vector c0 + jj of T) as
+// soon as it is final, so the stores drain while the later steps run.
+template <int EPT, bool VEC>
+__device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (*red)[64 * kPB], int& par,
+                                           gfloat* __restrict__ T, int R, int c0) {
 #pragma unroll
   for (int jj = 0; jj < kPB; jj++) {
     if (jj >= nv) break;
@@ -472,6 +474,7 @@ __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (
     const float nrm = sqrtf(s[0]) + 1e-30f, rn = 1.f / nrm;
 #pragma unroll
     for (int e = 0; e < EPT; e++) x[jj][e] = div_shared(x[jj][e], nrm, rn);
+    row_store<EPT, VEC>(T + (int64_t)(c0 + jj) * R, R, threadIdx.x, x[jj]);
     if (jj + 1 >= nv) break;
     float d[kPB];
 #pragma unroll
@@ -534,7 +537,10 @@ __device__ __forceinline__ void mgs_panel_body(gfloat* __restrict__ T, int R, in
   for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, v < nv, x[v]);
   int par = 0;
   if (jp >= 0) mgs_project<EPT, VEC, kPB>(T, R, jp, x, red, par);
-  if (lead) mgs_factor<EPT>(x, nv, red, par);
+  if (lead) {
+    mgs_factor<EPT, VEC>(x, nv, red, par, T, R, c0);
+    return;
+  }
 #pragma unroll
   for (int v = 0; v < kPB; v++)
     if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, x[v]);
