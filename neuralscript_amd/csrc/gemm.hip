@@ -175,10 +175,40 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
   tn = in / gsize;
 }
 
+// Plain epilogue C = acc * act'(aux) for one wave's 64x64 block (aux with
+// C's row and column indices, pitch ldaux): each 32x32 block's 16 aux values
+// load together, then its stores.  Its own loop nest, so that the main
+// epilogue's loops stay fully unrolled and the accumulators in registers.
+template <int CODE>
+__device__ __forceinline__ void store_act_grad(const floatx16 (&acc)[2][2], const GemmArgs& g, float* __restrict__ C,
+                                               int m0, int n0, int wm, int wn, int l32, int kh, int m_end) {
+#pragma unroll
+  for (int r = 0; r < 2; r++)
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int col = n0 + wn * 64 + c * 32 + l32;
+      const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
+      const bool cin = col < g.N;
+      const float* ap = g.aux + (int64_t)row0 * g.ldaux + col;
+      float* cp = C + (int64_t)row0 * g.ldc + col;
+      float au[16];
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int dr = 8 * (v >> 2) + (v & 3);
+        au[v] = cin && row0 + dr < m_end ? ap[(int64_t)dr * g.ldaux] : 0.f;
+      }
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int dr = 8 * (v >> 2) + (v & 3);
+        if (cin && row0 + dr < m_end) cp[(int64_t)dr * g.ldc] = acc[r][c][v] * act_deriv(au[v], CODE);
+      }
+    }
+}
+
 // opA(A)[m,k]: TA ? A[k*lda+m] : A[m*lda+k]   (KC for A <=> !TA)
 // opB(B)[k,n]: TB ? B[n*ldb+k] : B[k*ldb+n]   (KC for B <=>  TB)
-// PLAIN: no row gather/scatter, no row scale; epilogue kEpiAct (with the
-// pre-activation / activation pair when C2 is set) or kEpiAccum.
+// PLAIN: no row scatter, no row scale; epilogue kEpiAct (with the
+// pre-activation / activation pair when C2 is set), kEpiActGrad or kEpiAccum.
 // WMW = 2 / WNW = 2: 4x2 / 2x4 waves (512 threads), workgroup tile
 // 256 x 128 / 128 x 256: a quarter fewer operand loads and LDS stores per FLOP.
 template <bool TA, bool TB, bool VEC, bool PLAIN, int WMW, int WNW>
@@ -304,6 +334,12 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
   // Accumulator v of lane (l32, kh) in a 32x32 block sits at
   // row 8*(v/4) + 4*kh + v%4, column l32.
   if constexpr (PLAIN) {
+    if (g.mode == kEpiActGrad) {
+      // C = acc * relu'(aux): the only activation gradient the plain path
+      // takes (plain_act_grad)
+      store_act_grad<kActRelu>(acc, g, C, m0, n0, wm, wn, l32, kh, m_end);
+      return;
+    }
     // plain stores, the activation resolved once per 32x32 block
 #pragma unroll
     for (int r = 0; r < 2; r++)
@@ -394,6 +430,10 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Activation gradients the plain epilogue applies itself: ReLU's (the
+// training MLPs'); the others take the general epilogue.
+static bool plain_act_grad(const GemmArgs& g) { return g.mode == kEpiActGrad && g.aux && g.act == kActRelu; }
+
 int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t s) {
   if (in.M <= 0 || in.N <= 0 || batch <= 0) return 0;
   GemmArgs g = in;
@@ -406,9 +446,11 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
                   (!tB || !g.kseg);
   const bool vec = va && vb;
-  // plain epilogue: no row maps or scaling; activation, accumulate or the
-  // pre-activation / activation pair (kchunk partials are always kEpiAct)
-  const bool plain = !g.c_rows && !g.row_scale && (g.mode == kEpiAct || g.mode == kEpiAccum);
+  // plain epilogue: no row maps or scaling; activation, activation gradient,
+  // accumulate or the pre-activation / activation pair (kchunk partials are
+  // always kEpiAct)
+  const bool plain = !g.c_rows && !g.row_scale &&
+                     (g.mode == kEpiAct || g.mode == kEpiAccum || plain_act_grad(g));
   if (g.C2 && !(plain && g.mode == kEpiAct)) {
     set_error("gemm: the pre-activation / activation pair needs the plain activation epilogue");
     return -1;

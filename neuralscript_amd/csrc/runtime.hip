@@ -622,7 +622,7 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
   g.lda = D; g.ldb = D; g.ldc = D;
   g.sA = 0; g.sB = BS * D; g.sC = D * D;
   if (rt_gemm_ex(m, g, true, false, 3) != 0) return -1;
-  // dX = dQ Wq^T + dK Wk^T + dV Wv^T
+  // dX = dQ Wq^T + dK Wk^T + dV Wv^T: the second and third accumulate
   const float* Ws[3] = {Wq, Wk, Wv};
   for (int j = 0; j < 3; j++) {
     GemmArgs h;
