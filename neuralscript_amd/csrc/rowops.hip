@@ -312,6 +312,9 @@ __global__ __launch_bounds__(256) void softmax_xent_vec_kernel(const float* __re
 // held in registers (NV4 float4 per thread): logits and labels are read
 // once.  Same per-element operations as the reference (max, expf(x - max),
 // sum, divide, -logf(p) where y > 0, (p - y) / rows); sums over a fixed tree.
+// Logits, labels and the gradient stream through non-temporal loads and
+// stores (each byte is touched once): c5's 1.6 GB per step at 5.7 TB/s
+// instead of 4.8.
 template <int NV4>
 __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __restrict__ logits,
                                                                const float* __restrict__ labels,
@@ -321,16 +324,16 @@ __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __re
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t r = blockIdx.x;
   const int64_t C4 = C / 4;
-  const float4* xr = reinterpret_cast<const float4*>(logits + r * C);
-  const float4* yr = reinterpret_cast<const float4*>(labels + r * C);
-  float4 x[NV4], y[NV4];
+  const gfloat4* xr = reinterpret_cast<const gfloat4*>(as_global(logits + r * C));
+  const gfloat4* yr = reinterpret_cast<const gfloat4*>(as_global(labels + r * C));
+  fvec4 x[NV4], y[NV4];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < NV4; i++) {
     const int64_t c = t + 256 * i;
     const bool in = c < C4;
-    x[i] = in ? xr[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    y[i] = in ? yr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    x[i] = in ? __builtin_nontemporal_load(xr + c) : fvec4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    y[i] = in ? __builtin_nontemporal_load(yr + c) : fvec4{0.f, 0.f, 0.f, 0.f};
     mx = fmaxf(mx, fmaxf(fmaxf(x[i].x, x[i].y), fmaxf(x[i].z, x[i].w)));
   }
   mx = wave_max(mx);
@@ -340,7 +343,7 @@ __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __re
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV4; i++) {
-    x[i] = make_float4(expf(x[i].x - mx), expf(x[i].y - mx), expf(x[i].z - mx), expf(x[i].w - mx));
+    x[i] = fvec4{expf(x[i].x - mx), expf(x[i].y - mx), expf(x[i].z - mx), expf(x[i].w - mx)};
     s += (x[i].x + x[i].y) + (x[i].z + x[i].w);
   }
   s = wave_sum(s);
@@ -348,7 +351,7 @@ __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __re
   __syncthreads();
   s = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
   const float inv_rows = 1.f / (float)rows;
-  float4* gr = reinterpret_cast<float4*>(grad + r * C);
+  gfloat4* gr = reinterpret_cast<gfloat4*>(as_global(grad + r * C));
   float loss = 0.f;
 #pragma unroll
   for (int i = 0; i < NV4; i++) {
@@ -358,9 +361,11 @@ __global__ __launch_bounds__(256) void softmax_xent_row_kernel(const float* __re
     if (y[i].y > 0.f) loss -= logf(p1);
     if (y[i].z > 0.f) loss -= logf(p2);
     if (y[i].w > 0.f) loss -= logf(p3);
-    if (write_grad && c < C4)
-      gr[c] = make_float4((p0 - y[i].x) * inv_rows, (p1 - y[i].y) * inv_rows, (p2 - y[i].z) * inv_rows,
-                          (p3 - y[i].w) * inv_rows);
+    if (write_grad && c < C4) {
+      const fvec4 gv{(p0 - y[i].x) * inv_rows, (p1 - y[i].y) * inv_rows, (p2 - y[i].z) * inv_rows,
+                     (p3 - y[i].w) * inv_rows};
+      __builtin_nontemporal_store(gv, gr + c);
+    }
   }
   loss = wave_sum(loss);
   if (lane == 0) red[2][w] = loss;
