@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "common.h"
+#include "hostcopy.h"
 #include "kernels.h"
 #include "nship.h"
 #include "plan.h"
@@ -77,6 +78,7 @@ struct ns_model {
   std::vector<Buf> arena;         // per value id
   std::map<std::string, Buf> scratch;
   std::map<int, int64_t*> dev_idx;  // Index / Scatter index lists on the device, by result id
+  nship::HostStage stage;           // pinned staging of the host-pointer entry points' copies
   // profiling
   bool prof = false;
   std::vector<ProfEntry> pending;
@@ -988,8 +990,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
 int host_sync_weights(const ns_model* m) {
   if (!m->host_stale) return 0;
   ns_model* mm = const_cast<ns_model*>(m);
-  NSH_CHECK(hipStreamSynchronize(mm->stream));
-  NSH_CHECK(hipMemcpy(mm->h_w.data(), mm->d_w, mm->h_w.size() * sizeof(float), hipMemcpyDeviceToHost));
+  if (stage_d2h(mm->stage, mm->h_w.data(), mm->d_w, mm->h_w.size() * sizeof(float), mm->stream) != 0) return -1;
   mm->host_stale = false;
   return 0;
 }
@@ -1152,6 +1153,7 @@ ns_model* nsh_model_init(const nsh_plan* ph, const float* weights, size_t num_fl
 void nsh_model_free(ns_model* m) {
   if (!m) return;
   if (m->stream) hipStreamSynchronize(m->stream);
+  stage_free(m->stage);
   for (auto& b : m->arena) if (b.p) hipFree(b.p);
   for (auto& kv : m->scratch) if (kv.second.p) hipFree(kv.second.p);
   for (auto& kv : m->dev_idx) if (kv.second) hipFree(kv.second);
@@ -1191,11 +1193,11 @@ int nsh_eval_infer(ns_model* m, const float* input, float* output, size_t input_
   }
   Buf& xb = m->scratch["__x"];
   if (ensure(xb, input_numel) != 0) return -1;
-  NSH_CHECK(hipMemcpyAsync(xb.p, input, input_numel * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  if (stage_h2d(m->stage, xb.p, input, input_numel * sizeof(float), m->stream) != 0) return -1;
   float* res = nullptr;
   size_t n = 0;
   if (run_forward(m, xb.p, input_numel, &res, &n) != 0) return -1;
-  if (n) NSH_CHECK(hipMemcpyAsync(output, res, n * sizeof(float), hipMemcpyDeviceToHost, m->stream));
+  if (n && stage_d2h(m->stage, output, res, n * sizeof(float), m->stream) != 0) return -1;
   return sync(m);
 }
 
@@ -1377,8 +1379,9 @@ static int stage_train_inputs(ns_model* m, const float* input, const float* labe
   Buf& xb = m->scratch["__x"];
   Buf& yb = m->scratch["__y"];
   if (ensure(xb, input_numel) != 0 || ensure(yb, ny) != 0) return -1;
-  NSH_CHECK(hipMemcpyAsync(xb.p, input, input_numel * sizeof(float), hipMemcpyHostToDevice, m->stream));
-  NSH_CHECK(hipMemcpyAsync(yb.p, labels, ny * sizeof(float), hipMemcpyHostToDevice, m->stream));
+  if (stage_h2d(m->stage, xb.p, input, input_numel * sizeof(float), m->stream) != 0 ||
+      stage_h2d(m->stage, yb.p, labels, ny * sizeof(float), m->stream) != 0)
+    return -1;
   *dx = xb.p;
   *dy = yb.p;
   return 0;

@@ -206,9 +206,15 @@ class Model:
         if not self.h:
             raise NshipError(last_error())
 
-    def eval_infer(self, x):
+    def eval_infer(self, x, out=None):
+        """ns_eval_infer on host arrays; `out` (float32, contiguous, at least
+        output_numel floats) is written in place when given."""
         x = np.ascontiguousarray(x, dtype=np.float32).ravel()
-        out = np.empty(self.plan.output_numel(x.size), dtype=np.float32)
+        n = self.plan.output_numel(x.size)
+        if out is None:
+            out = np.empty(n, dtype=np.float32)
+        elif out.dtype != np.float32 or not out.flags.c_contiguous or out.size < n:
+            raise NshipError("eval_infer: out must be contiguous float32 with room for the output")
         check(lib().nsh_eval_infer(self.h, x.ctypes.data_as(_f32p), out.ctypes.data_as(_f32p), x.size),
               "eval_infer")
         return out
