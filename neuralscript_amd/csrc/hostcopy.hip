@@ -16,6 +16,8 @@
 #include <thread>
 #include <vector>
 
+#include <unistd.h>
+
 #include "common.h"
 
 namespace nship {
@@ -27,15 +29,18 @@ constexpr size_t kPoolMin = size_t(1) << 20;     // smaller host copies run on t
 
 // Process-wide helper threads for the host side of the staged copies.  One
 // copy at a time (callers on several models serialise on call_mu); the
-// calling thread takes part 0 and the helpers parts 1..n.
+// calling thread takes part 0 and the helpers parts 1..n.  The pool lives
+// until the process ends (never destroyed, so no join at exit); a child
+// process forked after it started copies on its calling thread alone, as
+// the helpers exist only in the parent.
 class CopyPool {
  public:
   static CopyPool& get() {
-    static CopyPool pool;
-    return pool;
+    static CopyPool* pool = new CopyPool();
+    return *pool;
   }
   void copy(void* dst, const void* src, size_t n) {
-    if (n < kPoolMin || th_.empty()) {
+    if (n < kPoolMin || th_.empty() || getpid() != pid_) {
       std::memcpy(dst, src, n);
       return;
     }
@@ -64,14 +69,6 @@ class CopyPool {
     const int helpers = hw > 1 ? (int)std::min(4u, hw - 1) : 0;
     for (int i = 0; i < helpers; i++) th_.emplace_back([this, i] { worker(i + 1); });
   }
-  ~CopyPool() {
-    {
-      std::lock_guard<std::mutex> lk(mu_);
-      stop_ = true;
-    }
-    work_cv_.notify_all();
-    for (auto& t : th_) t.join();
-  }
   // part p of the job: 64-byte aligned pieces of ceil(n / parts)
   static void run(const Job& j, int p) {
     const size_t per = ((j.n + j.parts - 1) / j.parts + 63) & ~size_t(63);
@@ -84,8 +81,7 @@ class CopyPool {
       Job j;
       {
         std::unique_lock<std::mutex> lk(mu_);
-        work_cv_.wait(lk, [&] { return stop_ || gen_ != seen; });
-        if (stop_) return;
+        work_cv_.wait(lk, [&] { return gen_ != seen; });
         seen = gen_;
         j = job_;
       }
@@ -102,7 +98,7 @@ class CopyPool {
   Job job_;
   unsigned long gen_ = 0;
   int pending_ = 0;
-  bool stop_ = false;
+  const pid_t pid_ = getpid();
 };
 
 // All slots or none: a failure part way frees what it allocated, so the
