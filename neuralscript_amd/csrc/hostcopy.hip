@@ -153,11 +153,11 @@ int stage_d2h(HostStage& st, void* host, const void* dev, size_t bytes, hipStrea
   auto issue = [&](size_t i) -> int {
     const int k = (int)(i % kStageSlots);
     const size_t off = i * kStageChunk, len = std::min(kStageChunk, bytes - off);
+    NSH_CHECK(hipStreamWaitEvent(s, st.ev[k], 0));  // the slot's last DMA may be on another stream
     NSH_CHECK(hipMemcpyAsync(st.slot[k], d + off, len, hipMemcpyDeviceToHost, s));
     NSH_CHECK(hipEventRecord(st.ev[k], s));
     return 0;
   };
-  // the slots' previous DMAs (a staged upload) are ordered before these on s
   for (size_t i = 0; i < std::min<size_t>(kStageSlots, n); i++)
     if (issue(i) != 0) return -1;
   for (size_t i = 0; i < n; i++) {

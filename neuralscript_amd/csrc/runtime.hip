@@ -79,6 +79,14 @@ struct ns_model {
   std::map<std::string, Buf> scratch;
   std::map<int, int64_t*> dev_idx;  // Index / Scatter index lists on the device, by result id
   nship::HostStage stage;           // pinned staging of the host-pointer entry points' copies
+  // Host labels of a host-pointer train call, uploaded when the loss first
+  // needs them (on copy_stream, so the upload overlaps the forward pass)
+  const float* labels_host = nullptr;
+  float* labels_dev = nullptr;
+  size_t labels_bytes = 0;
+  hipStream_t copy_stream = nullptr;
+  hipEvent_t labels_ev = nullptr;
+  hipEvent_t before_ev = nullptr;   // the model's stream before this call's kernels
   // profiling
   bool prof = false;
   std::vector<ProfEntry> pending;
@@ -730,6 +738,25 @@ int64_t ce_classes(const Func& F, const Plan& P, int preds) {
   return c > 0 ? c : P.in_cols;
 }
 
+// Uploads deferred host labels (a host-pointer train call) on the copy
+// stream and makes the model's stream wait for them.  Called by the ops that
+// read the labels: the kernels of the forward pass, already enqueued, run
+// while the host stages the upload.
+int labels_ready(ns_model* m) {
+  if (!m->labels_host) return 0;
+  const float* host = m->labels_host;
+  m->labels_host = nullptr;
+  if (!m->copy_stream) NSH_CHECK(hipStreamCreateWithFlags(&m->copy_stream, hipStreamNonBlocking));
+  if (!m->labels_ev) NSH_CHECK(hipEventCreateWithFlags(&m->labels_ev, hipEventDisableTiming));
+  // work enqueued before this call (which may still read the label buffer)
+  // finishes before the upload overwrites it
+  NSH_CHECK(hipStreamWaitEvent(m->copy_stream, m->before_ev, 0));
+  if (stage_h2d(m->stage, m->labels_dev, host, m->labels_bytes, m->copy_stream) != 0) return -1;
+  NSH_CHECK(hipEventRecord(m->labels_ev, m->copy_stream));
+  NSH_CHECK(hipStreamWaitEvent(m->stream, m->labels_ev, 0));
+  return 0;
+}
+
 int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, float lr, bool train_mode,
               float** d_loss) {
   if (ensure_device_current(m) != 0) return -1;
@@ -788,6 +815,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
         const int64_t rows = (int64_t)(n / (size_t)C);
         fr.numel[F.y] = n;
         fr.ptr[F.y] = const_cast<float*>(d_y);
+        if (labels_ready(m) != 0) return -1;
         float* rl = scratch(m, "row_loss", (size_t)std::max<int64_t>(rows, 1));
         if (!rl) return -1;
         float* grad = nullptr;
@@ -821,6 +849,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             float* rl = scratch(m, "row_loss", (size_t)std::max<int64_t>(rows, 1));
             float* tmp = scratch(m, "loss_tmp", 1);
             if (!rl || !tmp) return -1;
+            if (labels_ready(m) != 0) return -1;
             Prof p(m, "softmax_xent");
             if (launch_softmax_xent(fr.ptr[I.in[0]], d_y, grad, rl, tmp, rows, C, true, s) != 0) return -1;
             if ((size_t)(rows * C) < n && launch_fill(grad + rows * C, (int64_t)n - rows * C, 0.f, s) != 0) return -1;
@@ -1153,7 +1182,11 @@ ns_model* nsh_model_init(const nsh_plan* ph, const float* weights, size_t num_fl
 void nsh_model_free(ns_model* m) {
   if (!m) return;
   if (m->stream) hipStreamSynchronize(m->stream);
+  if (m->copy_stream) hipStreamSynchronize(m->copy_stream);
   stage_free(m->stage);
+  if (m->labels_ev) hipEventDestroy(m->labels_ev);
+  if (m->before_ev) hipEventDestroy(m->before_ev);
+  if (m->copy_stream) hipStreamDestroy(m->copy_stream);
   for (auto& b : m->arena) if (b.p) hipFree(b.p);
   for (auto& kv : m->scratch) if (kv.second.p) hipFree(kv.second.p);
   for (auto& kv : m->dev_idx) if (kv.second) hipFree(kv.second);
@@ -1379,9 +1412,13 @@ static int stage_train_inputs(ns_model* m, const float* input, const float* labe
   Buf& xb = m->scratch["__x"];
   Buf& yb = m->scratch["__y"];
   if (ensure(xb, input_numel) != 0 || ensure(yb, ny) != 0) return -1;
-  if (stage_h2d(m->stage, xb.p, input, input_numel * sizeof(float), m->stream) != 0 ||
-      stage_h2d(m->stage, yb.p, labels, ny * sizeof(float), m->stream) != 0)
-    return -1;
+  if (!m->before_ev) NSH_CHECK(hipEventCreateWithFlags(&m->before_ev, hipEventDisableTiming));
+  NSH_CHECK(hipEventRecord(m->before_ev, m->stream));
+  if (stage_h2d(m->stage, xb.p, input, input_numel * sizeof(float), m->stream) != 0) return -1;
+  // the labels follow when the loss needs them (labels_ready)
+  m->labels_host = labels;
+  m->labels_dev = yb.p;
+  m->labels_bytes = ny * sizeof(float);
   *dx = xb.p;
   *dy = yb.p;
   return 0;
@@ -1396,7 +1433,9 @@ int nsh_train_step(ns_model* m, const float* input, const float* labels, size_t 
   float *dx = nullptr, *dy = nullptr;
   if (stage_train_inputs(m, input, labels, input_numel, &dx, &dy) != 0) return -1;
   float loss = 0.f;
-  if (nsh_train_step_device(m, dx, dy, input_numel, &loss, lr) != 0) return -1;
+  const int rc = nsh_train_step_device(m, dx, dy, input_numel, &loss, lr);
+  m->labels_host = nullptr;  // not read by this plan, or consumed
+  if (rc != 0) return -1;
   if (loss_out) *loss_out = loss;
   return 0;
 }
@@ -1414,7 +1453,9 @@ int nsh_objective_loss(ns_model* m, const float* input, const float* labels, siz
   float *dx = nullptr, *dy = nullptr;
   if (stage_train_inputs(m, input, labels, input_numel, &dx, &dy) != 0) return -1;
   float* d_loss = nullptr;
-  if (run_train(m, dx, input_numel, dy, 0.f, false, &d_loss) != 0) return -1;
+  const int rc = run_train(m, dx, input_numel, dy, 0.f, false, &d_loss);
+  m->labels_host = nullptr;
+  if (rc != 0) return -1;
   float loss = 0.f;
   NSH_CHECK(hipMemcpyAsync(&loss, d_loss, sizeof(float), hipMemcpyDeviceToHost, m->stream));
   if (sync(m) != 0) return -1;
