@@ -17,11 +17,16 @@ def ws(r, c):
     return DA(runtime.lib().nsh_op_muon_workspace(r, c) // 4 + 64)
 
 
+# Register panels (512 threads, up to 16 elements a thread): every vector
+# length class, 1 (<= 512), 2 (<= 1024), 4, 8 (<= 4096) and 16 (<= 8192)
+# elements a thread, with float4 rows (length % 4 == 0) and scalar ones, and
+# ragged last panels (vector counts not multiples of 8).
 # (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001): vectors
 # longer than 8192 floats take the sliced path (2048-float slices, one launch
 # per column) instead of the register panels; odd lengths take its scalar
 # loads, 19 vectors a ragged last batch of 3
 @pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192),
+                                 (1000, 40), (3001, 24), (4096, 20), (5001, 24), (24, 6000), (8192, 9),
                                  (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001)])
 def test_orthonormalize_matches_oracle_mgs(r, c):
     """Q within the fp32 bar (1e-5 + 1e-4 |ref|) of the oracle's.  A square
