@@ -47,8 +47,8 @@ def test_layernorm_backward(rows, last):
     helpers.assert_close(dx.to_host(), oracle.layernorm_grad(d, x, last), f"layernorm_grad {rows}x{last}")
 
 
-@pytest.mark.parametrize("rows,C", [(1, 2), (129, 10), (512, 8192), (64, 2048), (33, 4000), (7, 12288), (5, 2050),
-                                    (16387, 16)])
+@pytest.mark.parametrize("rows,C", [(1, 2), (129, 10), (512, 8192), (64, 2048), (100, 4096), (33, 4000), (7, 12288),
+                                    (5, 2050), (16387, 16)])
 def test_softmax_cross_entropy_and_seed(rows, C):
     x = synth.normal(rows + C, rows * C, 3.0)
     y = synth.one_hot(synth.token_ids(rows, rows, C), C)
