@@ -584,7 +584,12 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
                         const uint8_t* active, const MoeWork& w, const MoeBwdWork& b, float* dx, float* dWg,
                         float* dWe1, float* dWe2, int64_t M, int64_t D, int64_t H, int64_t E, hipStream_t s,
                         int phases) {
-  if (M <= 0) return 0;
+  if (M <= 0) {  // no tokens: the weight gradients are empty sums
+    if (dWg && launch_fill(dWg, D * E, 0.f, s) != 0) return -1;
+    if (dWe1 && launch_fill(dWe1, E * D * H, 0.f, s) != 0) return -1;
+    if (dWe2 && launch_fill(dWe2, E * H * D, 0.f, s) != 0) return -1;
+    return 0;
+  }
   const int* nrows = w.seg + E;
   if (phases & kMoeBwdGrouped) {
   // dpre2[pos] = dout[perm[pos]] . We2[e]^T

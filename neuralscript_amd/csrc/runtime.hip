@@ -607,7 +607,8 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
   const float* Wk = fr.ptr[I.in[3]];
   const float* Wv = fr.ptr[I.in[4]];
   const float* Wo = fr.ptr[I.in[5]];
-  if (BS == 0) return 0;
+  if (BS == 0)  // no tokens: every weight gradient is an empty sum
+    return launch_fill(out->dW3, 3 * D * D, 0.f, s) != 0 || launch_fill(out->dWo, D * D, 0.f, s) != 0 ? -1 : 0;
   {
     Prof p(m, "gemm");
     // dPre = dout Wo^T

@@ -158,6 +158,10 @@ def empty(n):
     return np.empty(int(n), dtype=np.float32)
 
 
+def zeros(n):
+    return np.zeros(int(n), dtype=np.float32)
+
+
 # ---------------------------------------------------------------------------
 # kernel wrappers (flat float32 arrays in, flat arrays out)
 # ---------------------------------------------------------------------------
@@ -262,7 +266,10 @@ def attention_fwd_rows(x, Wq, Wk, Wv, Wo, rows, BS, D, H):
 
 
 def attention_bwd(dout, x, Wq, Wk, Wv, Wo, BS, D, H):
-    dX, dWq, dWk, dWv, dWo = empty(BS * D), empty(D * D), empty(D * D), empty(D * D), empty(D * D)
+    # zeros: with no tokens ns_attention_bwd returns before writing
+    # (codegen.cpp:1789), leaving the train core's buffers as resized, which
+    # is zero on a fresh context
+    dX, dWq, dWk, dWv, dWo = empty(BS * D), zeros(D * D), zeros(D * D), zeros(D * D), zeros(D * D)
     lib().or_attention_bwd(fp(dout), fp(x), fp(Wq), fp(Wk), fp(Wv), fp(Wo), fp(dX), fp(dWq),
                            fp(dWk), fp(dWv), fp(dWo), BS, D, H)
     return dX, dWq, dWk, dWv, dWo

@@ -63,6 +63,27 @@ def test_train_steps_match_reference_fixture(case):
     lib.free(m)
 
 
+@pytest.mark.parametrize("name", ["mlpt", "c5s", "moet", "moeb", "drp", "c5a"])
+def test_train_step_on_an_empty_batch(name):
+    """Zero rows: the reference's loss is 0/0 (NaN) and every gradient an
+    empty sum, so the optimizer step applies only its decay terms (Muon of a
+    zero matrix gives Q = 0; AdamW of g = 0 moves nothing but the decay)."""
+    print(f"empty train step {name}", flush=True)
+    net = oracle.Net(helpers.ir_text(name))
+    w = helpers.net_weights(name, 3)
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    om = oracle.Model(net, w)
+    empty = np.zeros(0, np.float32)
+    loss = lib.train_step(m, empty, empty, 0.02)
+    ref = om.train_step(empty, empty, 0.02)
+    assert np.isnan(loss) and np.isnan(ref), (loss, ref)
+    got = lib.get_weights(m)
+    print(f"  weights bit-identical to the oracle's: {helpers.bitwise_equal(got, om.w)}")
+    helpers.assert_close(got, np.asarray(om.w, np.float32), f"{name} weights after an empty step")
+    lib.free(m)
+
+
 def test_objective_does_not_mutate_weights():
     name, rows, seed = "c5t", 33, 108
     net, x, y = case_inputs(name, rows, seed)
