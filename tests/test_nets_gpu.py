@@ -67,6 +67,48 @@ def test_forward_of_an_empty_batch(name):
     lib.free(m)
 
 
+@pytest.mark.parametrize("name", ["c1", "mlpt", "c2s", "xor", "dmv", "smt", "bop"])
+def test_forward_of_a_ragged_batch(name):
+    """input_numel not a multiple of in_cols: the reference takes
+    floor(numel / in_cols) rows (codegen.cpp:1257-1265 with M = numel / K)
+    and leaves the partial row unread; outputs against the oracle on the same
+    ragged buffer."""
+    print(f"ragged batch {name}", flush=True)
+    net = oracle.Net(helpers.ir_text(name))
+    w = helpers.net_weights(name, 4)
+    x = helpers.net_inputs(net, name, 9, 5)
+    xr = np.concatenate([x, np.full(net.in_cols - 1, 0.5, np.float32)])
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    out = lib.eval_infer(m, xr)
+    ref = oracle.Model(net, w).eval_infer(xr)
+    lib.free(m)
+    helpers.assert_close(out[: ref.size], ref, f"{name} ragged forward")
+
+
+@pytest.mark.parametrize("name", ["xor"])
+def test_train_step_on_a_ragged_batch(name):
+    """Training with input_numel not a multiple of in_cols (a net whose
+    weights all take AdamW, so the step is determined; Muon on a six-row
+    gradient is not): loss and weights after three steps against the oracle
+    on the same ragged buffer."""
+    print(f"ragged train {name}", flush=True)
+    net = oracle.Net(helpers.ir_text(name))
+    w = helpers.net_weights(name, 4)
+    rows = 6
+    x = helpers.net_inputs(net, name, 9, rows)
+    xr = np.concatenate([x, np.full(net.in_cols - 1, 0.5, np.float32)])
+    y = helpers.net_labels(net, 10, rows)
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    om = oracle.Model(net, w)
+    for _ in range(3):
+        loss, ref = lib.train_step(m, xr, y, 0.05), om.train_step(xr, y, 0.05)
+        helpers.assert_close(np.float32([loss]), np.float32([ref]), f"{name} ragged loss")
+    helpers.assert_close(lib.get_weights(m), np.asarray(om.w, np.float32), f"{name} ragged weights")
+    lib.free(m)
+
+
 def test_c2_full_size_rows_match_oracle():
     """Config 2 at its full batch (8192 x 1024 -> 4096 -> 4096 -> 1024, GELU);
     the oracle recomputes 96 rows spread over the batch (rows are independent)."""
