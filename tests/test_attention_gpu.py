@@ -26,7 +26,7 @@ def core_ref(Q, K, V, S, D, H):
 
 
 @pytest.mark.parametrize("S,D,H", [(1, 64, 1), (100, 128, 2), (333, 64, 1), (1024, 1024, 16), (300, 64, 2),
-                                   (257, 16, 2), (90, 64, 8), (2048, 512, 8)])
+                                   (257, 16, 2), (90, 64, 8), (2048, 512, 8), (100, 128, 1), (77, 192, 2)])
 def test_attention_core_matches_float64(S, D, H):
     print(f"attention core S={S} D={D} H={H}", flush=True)
     Q, K, V = (synth.normal(S * 10 + i, S * D, 1.0) for i in range(3))
@@ -57,7 +57,7 @@ def core_bwd_ref(Q, K, V, dO, S, D, H):
 
 
 @pytest.mark.parametrize("S,D,H", [(64, 128, 2), (192, 128, 2), (100, 128, 2), (256, 64, 2), (130, 64, 2),
-                                   (90, 64, 8), (1024, 512, 8), (2048, 512, 8)])
+                                   (90, 64, 8), (1024, 512, 8), (2048, 512, 8), (100, 128, 1), (77, 192, 2)])
 @pytest.mark.parametrize("store_ds", [0, 1])
 def test_attention_core_backward_matches_float64(S, D, H, store_ds):
     """Flash backward (head size 32/64: key-parallel dK/dV pass, then dQ

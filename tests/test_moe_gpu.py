@@ -68,7 +68,8 @@ def test_moe_lifecycle_matches_reference_fixture():
 
 
 @pytest.mark.parametrize("M,D,E,H,mask", [(1000, 64, 8, 96, None), (3000, 128, 64, 64, None),
-                                          (777, 64, 16, 32, "some"), (513, 32, 130, 16, None)])
+                                          (777, 64, 16, 32, "some"), (513, 32, 130, 16, None),
+                                          (600, 32, 256, 16, "some")])
 def test_moe_routing_is_bit_exact(M, D, E, H, mask):
     print(f"moe routing M={M} D={D} E={E} H={H}", flush=True)
     ir = ("ns.func @MOE {\n"
