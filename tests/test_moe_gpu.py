@@ -180,6 +180,35 @@ def test_lifecycle_after_training_keeps_trained_weights():
     lib.free(m)
 
 
+def test_moe_forward_with_every_expert_killed():
+    """ns_expert_kill may take the live count to zero (codegen.cpp:2590-2626).
+    The reference's forward then routes every token to expert -1 and reads
+    outside its weights (no defined result); this backend outputs zeros and
+    reports best = -1, and a later birth makes the layer route again."""
+    name = "c4k"
+    case = next(c for c in CASES if c[0] == name)
+    net, x, _ = case_inputs(name, case[1], case[2])
+    lib = runtime.net_lib(name)
+    w = helpers.net_weights(name, case[2])
+    m = lib.init(w)
+    om = oracle.Model(net, w)
+    for k in range(net.moe["E"]):
+        n = lib.lib.ns_expert_kill(m, k)
+        om.expert_kill(k)
+    assert n == 0
+    # the forward writes M x D floats (x's size); output_numel's F3 quirk
+    # sizes the host buffer larger
+    out = lib.eval_infer(m, x)[: x.size]
+    assert np.all(out == 0.0), "no live expert: the MoE output must be zero"
+    # birth finds no live source within its tries and copies the last drawn
+    # slot (codegen.cpp:2565-2590), as the oracle restates
+    assert lib.lib.ns_expert_birth(m, 1) == om.expert_birth(1) == 1
+    assert helpers.bitwise_equal(lib.get_weights(m), om.w), "birth from no live expert"
+    ref = om.eval_infer(x)
+    helpers.assert_close(lib.eval_infer(m, x)[: ref.size], ref, "forward after the birth")
+    lib.free(m)
+
+
 def test_moe_checkpoint_tail_matches_reference(tmp_path):
     """NSM2 with the MoE tail (codegen.cpp:2501-2557) on c4k after birth,
     merge and kill: the saved file is byte-identical to the reference
