@@ -109,6 +109,34 @@ def test_train_step_on_a_ragged_batch(name):
     lib.free(m)
 
 
+@pytest.mark.parametrize("name", ["c1", "mlpt", "c2s", "smt"])
+def test_forward_propagates_inf_and_nan_like_the_reference(name):
+    """Rows holding +inf, -inf or NaN inputs: the non-finite outputs sit where
+    the oracle's do (same sign for infinities; an infinity and its opposite
+    in one sum give NaN in any order), and the rows without special values
+    match to the fp32 bar."""
+    print(f"special values {name}", flush=True)
+    net = oracle.Net(helpers.ir_text(name))
+    w = helpers.net_weights(name, 4)
+    rows = 8
+    x = helpers.net_inputs(net, name, 9, rows).reshape(rows, net.in_cols).copy()
+    x[1, 0] = np.inf
+    x[3, -1] = -np.inf
+    x[5, 1] = np.nan
+    x[6, 0], x[6, 1] = np.inf, -np.inf
+    lib = runtime.net_lib(name)
+    m = lib.init(w)
+    out = lib.eval_infer(m, x.ravel())
+    ref = oracle.Model(net, w).eval_infer(x.ravel())
+    lib.free(m)
+    out = out[: ref.size].reshape(rows, -1)
+    ref = ref.reshape(rows, -1)
+    assert np.array_equal(np.isnan(out), np.isnan(ref)), "NaN positions differ"
+    assert np.array_equal(np.isposinf(out), np.isposinf(ref)) and np.array_equal(np.isneginf(out), np.isneginf(ref))
+    clean = [r for r in range(rows) if r not in (1, 3, 5, 6)]
+    helpers.assert_close(out[clean], ref[clean], f"{name} rows without special values")
+
+
 def test_c2_full_size_rows_match_oracle():
     """Config 2 at its full batch (8192 x 1024 -> 4096 -> 4096 -> 1024, GELU);
     the oracle recomputes 96 rows spread over the batch (rows are independent)."""
