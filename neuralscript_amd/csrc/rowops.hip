@@ -401,7 +401,7 @@ __global__ __launch_bounds__(1024) void mean_loss_kernel(const float* __restrict
 int launch_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
                         int64_t rows, int64_t C, bool write_grad, hipStream_t s) {
   // no whole row: the reference's mean is 0.f / 0 (codegen.cpp:1612), a NaN
-  if (rows <= 0) return launch_fill(loss, 1, __builtin_nanf(""), s);
+  if (rows <= 0) return loss ? launch_fill(loss, 1, __builtin_nanf(""), s) : 0;
   const bool vec = C % 4 == 0 && ((uintptr_t)logits | (uintptr_t)labels | (uintptr_t)grad) % 16 == 0;
   const int64_t nv4 = ceil_div(C / 4, 256);
   if (vec && C >= 2048 && nv4 <= 8) {

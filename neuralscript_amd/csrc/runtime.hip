@@ -1597,28 +1597,43 @@ int nsh_op_gemm_splitk(const float* A, const float* B, float* C, int64_t M, int6
     return 0;                                     \
   } while (0)
 
+// Argument checks of the op entry points, before any device work: a null
+// buffer that a nonempty call would touch, or a negative size, is an error.
+#define NSH_OP_REQUIRE(cond, what)                          \
+  do {                                                      \
+    if (!(cond)) {                                          \
+      set_error(std::string(what) + ": bad arguments");     \
+      return -1;                                            \
+    }                                                       \
+  } while (0)
+
 int nsh_op_embedding(const float* W, const float* idx, float* out, int64_t n, int64_t V, int64_t D) {
+  NSH_OP_REQUIRE(n >= 0 && D >= 0 && (n == 0 || D == 0 || (W && idx && out && V > 0)), "embedding");
   if (launch_embedding(W, idx, out, n, V, D, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 
 int nsh_op_layernorm(const float* x, float* y, int64_t rows, int64_t last) {
+  NSH_OP_REQUIRE(rows >= 0 && (rows == 0 || (x && y)), "layernorm");
   if (last <= 0 || launch_layernorm(x, y, rows, last, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 
 int nsh_op_layernorm_grad(const float* dout, const float* x, float* dx, int64_t rows, int64_t last) {
+  NSH_OP_REQUIRE(rows >= 0 && (rows == 0 || (dout && x && dx)), "layernorm_grad");
   if (last <= 0 || launch_layernorm_grad(dout, x, dx, rows, last, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 
 int nsh_op_softmax_xent(const float* logits, const float* labels, float* grad, float* row_loss, float* loss,
                         int64_t rows, int64_t C) {
+  NSH_OP_REQUIRE(rows <= 0 || (logits && labels && row_loss && loss && C > 0), "softmax_xent");
   if (launch_softmax_xent(logits, labels, grad, row_loss, loss, rows, C, grad != nullptr, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
 
 int nsh_op_act_grad(const float* din, const float* pre, float* dout, int64_t n, int act) {
+  NSH_OP_REQUIRE(n >= 0 && (n == 0 || (din && pre && dout)), "act_grad");
   if (launch_act_grad(din, pre, dout, n, act, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
@@ -1627,6 +1642,7 @@ size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V) { return embedding_
 
 int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                           void* workspace) {
+  NSH_OP_REQUIRE(n >= 0 && V >= 0 && D >= 0 && (V * D == 0 || dW) && (n == 0 || (dout && idx)), "embedding_grad");
   if (!workspace || launch_embedding_grad(dout, idx, dW, n, V, D, (int*)workspace, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
@@ -1738,6 +1754,7 @@ int nsh_bench_copy(const float* src, float* dst, int64_t n, int reps, double* gb
 }
 
 int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr) {
+  NSH_OP_REQUIRE(n >= 0 && (n == 0 || (w && g && m && v)), "adamw_step");
   const float b1t = 1.f - powf(0.9f, (float)t), b2t = 1.f - powf(0.999f, (float)t);
   if (launch_adamw(w, g, m, v, n, lr, b1t, b2t, nullptr) != 0) return -1;
   NSH_OP_DONE();
@@ -1745,6 +1762,7 @@ int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, i
 
 int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
                          int64_t D, int64_t H) {
+  NSH_OP_REQUIRE(S >= 0 && (S == 0 || (Q && K && V && ctx)), "attention_fwd");
   if (launch_attention_fwd(Q, K, V, ctx, lse, S, D, H, D, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }

@@ -93,3 +93,28 @@ def test_moe_plan_without_initial_experts_is_rejected(name):
     with pytest.raises(runtime.NshipError, match="initial"):
         runtime.Plan(plain)
     runtime.Plan(text)  # the attribute-preserving text parses
+
+
+# Each op entry point with a null buffer that a nonempty call would touch:
+# -1 and a message, decided before any device work (so it runs without a GPU).
+NULL_CALLS = [
+    ("nsh_op_embedding", (None, None, None, 4, 10, 8)),
+    ("nsh_op_layernorm", (None, None, 4, 8)),
+    ("nsh_op_layernorm_grad", (None, None, None, 4, 8)),
+    ("nsh_op_softmax_xent", (None, None, None, None, None, 4, 8)),
+    ("nsh_op_act_grad", (None, None, None, 16, 1)),
+    ("nsh_op_embedding_grad", (None, None, None, 4, 10, 8, None)),
+    ("nsh_op_adamw_step", (None, None, None, None, 16, 1, 0.01)),
+    ("nsh_op_attention_fwd", (None, None, None, None, None, 16, 64, 1)),
+    ("nsh_op_attention_bwd", (None,) * 9 + (16, 64, 1, 0, None)),
+    ("nsh_op_orthonormalize", (None, None, 16, 8, None)),
+    ("nsh_op_muon_step", (None, None, 16, 8, 0.01, None)),
+    ("nsh_op_gemm", (None, None, None, 4, 4, 4, 4, 4, 4, 0, 0, 0)),
+]
+
+
+@pytest.mark.parametrize("name,args", NULL_CALLS, ids=[c[0] for c in NULL_CALLS])
+def test_op_entry_points_reject_null_buffers(name, args):
+    L = runtime.lib()
+    assert getattr(L, name)(*args) == -1
+    assert runtime.last_error(), f"{name}: no error message"
