@@ -50,21 +50,20 @@ struct KVTile {
   static constexpr int kVec = kBK * DK / 4;    // float4 per tile
   static constexpr int kPer = kVec / 256;      // float4 per thread
   float4 k[kPer], v[kPer];
+  int lim = 0;  // tile rows below lim exist
 
+  // Rows past the end load a clamped row; store() zeroes them, so nothing
+  // between load() and store() waits for the loads.
   __device__ void load(const float* __restrict__ K, const float* __restrict__ V, int64_t ld, int hcol, int key0,
                        int S, int t) {
+    lim = S - key0;
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int idx = t + 256 * i;
       const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
-      // rows past the end load a clamped row and are zeroed by a select
-      const int gk = key0 + key;
-      const bool in = gk < S;
-      const int64_t row = in ? gk : S - 1;
-      const float4 a = *reinterpret_cast<const float4*>(K + row * ld + hcol + c);
-      const float4 b = *reinterpret_cast<const float4*>(V + row * ld + hcol + c);
-      k[i] = keep4(in, a);
-      v[i] = keep4(in, b);
+      const int64_t row = key < lim ? key0 + key : S - 1;
+      k[i] = *reinterpret_cast<const float4*>(K + row * ld + hcol + c);
+      v[i] = *reinterpret_cast<const float4*>(V + row * ld + hcol + c);
     }
   }
   __device__ void store(float* __restrict__ ks, int t) const {
@@ -73,35 +72,37 @@ struct KVTile {
     for (int i = 0; i < kPer; i++) {
       const int idx = t + 256 * i;
       const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
-      *reinterpret_cast<float4*>(ks + key * P + c) = k[i];
-      *reinterpret_cast<float4*>(vs + key * P + c) = v[i];
+      *reinterpret_cast<float4*>(ks + key * P + c) = keep4(key < lim, k[i]);
+      *reinterpret_cast<float4*>(vs + key * P + c) = keep4(key < lim, v[i]);
     }
   }
 };
 
 // One K or V tile (64 keys x DK) in registers on its way to LDS (row pitch
-// DK + 4); rows past the end load a clamped row and are zeroed.
+// DK + 4); rows past the end load a clamped row and are zeroed by store(),
+// so nothing between load() and store() waits for the loads.
 template <int DK, int NTH>
 struct HalfTile {
   static constexpr int P = DK + 4;
   static constexpr int kPer = kBK * DK / 4 / NTH;
   float4 r[kPer];
+  int lim = 0;  // tile rows below lim exist
   __device__ void load(const float* __restrict__ X, int64_t ld, int hcol, int key0, int S, int t) {
+    lim = S - key0;
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int idx = t + NTH * i;
       const int key = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
-      const int gk = key0 + key;
-      const bool in = gk < S;
-      const int64_t row = in ? gk : S - 1;
-      r[i] = keep4(in, *reinterpret_cast<const float4*>(X + row * ld + hcol + c));
+      const int64_t row = key < lim ? key0 + key : S - 1;
+      r[i] = *reinterpret_cast<const float4*>(X + row * ld + hcol + c);
     }
   }
   __device__ void store(float* __restrict__ xs, int t) const {
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int idx = t + NTH * i;
-      *reinterpret_cast<float4*>(xs + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = r[i];
+      const int key = idx / (DK / 4);
+      *reinterpret_cast<float4*>(xs + key * P + (idx % (DK / 4)) * 4) = keep4(key < lim, r[i]);
     }
   }
 };
@@ -347,19 +348,19 @@ struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
   static constexpr int kPer = 64 * DK / 4 / 256;  // float4 per thread per matrix
   float4 q[kPer], g[kPer];
   float l = 0.f, d = 0.f;
+  int lim = 0;  // tile rows below lim exist
+  // Rows past the end load a clamped row; store() zeroes them, so nothing
+  // between load() and store() waits for the loads.
   __device__ void load(const float* __restrict__ Q, const float* __restrict__ dO, const float* __restrict__ lse,
                        const float* __restrict__ delta, int64_t ld, int hcol, int hS, int q0, int S, int t) {
+    lim = S - q0;
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
       const int idx = t + 256 * i;
       const int r = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
-      const int gq = q0 + r;
-      const bool in = gq < S;
-      const int64_t row = in ? gq : S - 1;
-      const float4 a = *reinterpret_cast<const float4*>(Q + row * ld + hcol + c);
-      const float4 b = *reinterpret_cast<const float4*>(dO + row * ld + hcol + c);
-      q[i] = keep4(in, a);
-      g[i] = keep4(in, b);
+      const int64_t row = r < lim ? q0 + r : S - 1;
+      q[i] = *reinterpret_cast<const float4*>(Q + row * ld + hcol + c);
+      g[i] = *reinterpret_cast<const float4*>(dO + row * ld + hcol + c);
     }
     if (t < 64) {
       const int gq = q0 + t;
@@ -373,8 +374,8 @@ struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
     for (int i = 0; i < kPer; i++) {
       const int idx = t + 256 * i;
       const int r = idx / (DK / 4), c = (idx % (DK / 4)) * 4;
-      *reinterpret_cast<float4*>(sm + r * P + c) = q[i];
-      *reinterpret_cast<float4*>(sm + 64 * P + r * P + c) = g[i];
+      *reinterpret_cast<float4*>(sm + r * P + c) = keep4(r < lim, q[i]);
+      *reinterpret_cast<float4*>(sm + 64 * P + r * P + c) = keep4(r < lim, g[i]);
     }
     if (t < 64) {
       sm[2 * 64 * P + t] = l;
@@ -608,45 +609,23 @@ __global__ __launch_bounds__(256) void flash_bwd_dq_kernel(const float* __restri
   }
 }
 
-// One 64-key step of flash_bwd_dq_ds_kernel: the K tile (float4 i of thread
-// t is key (t + 256 i) / (DK/4), dims 4 ((t + 256 i) % (DK/4))) and this
-// lane's dS operands, d[4 kb + j] = keys key0 + 32 kb + 8 j + 4 kh + (0..3)
-// of its query row (drow already includes the 4 kh offset).
-template <int DK>
-struct DsTile {
-  static constexpr int P = DK + 4;
-  static constexpr int kPer = kBK * DK / 4 / 256;
-  float4 k[kPer], d[8];
-  __device__ void load(const float* __restrict__ K, const float* __restrict__ drow, int64_t ld, int hcol, int key0,
-                       bool qin, int t) {
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int idx = t + 256 * i;
-      k[i] = *reinterpret_cast<const float4*>(K + (int64_t)(key0 + idx / (DK / 4)) * ld + hcol + (idx % (DK / 4)) * 4);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-      d[i] = keep4(qin, *reinterpret_cast<const float4*>(drow + key0 + 32 * (i >> 2) + 8 * (i & 3)));
-  }
-  __device__ void store_k(float* __restrict__ ks, int t) const {
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-      const int idx = t + 256 * i;
-      *reinterpret_cast<float4*>(ks + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = k[i];
-    }
-  }
-};
-
 // dQ = scale * dS K from the stored dS (S % 64 == 0): the dq kernel's
 // transposed product dQ^T += K^T dS^T without recomputing S and dP.  Lane =
-// query; its dS operands are 8 float4 per 64-key tile read straight from its
-// row (prefetched one tile ahead); K tiles go through LDS.
+// query; its dS operands of a 64-key tile are 8 float4 read straight from its
+// row, dlo/dhi[j] = keys key0 + 32 kb + 8 j + 4 kh + (0..3) for kb = 0/1
+// (drow includes the 4 kh offset; a lane past the end reads row S - 1 and its
+// operands are zeroed where they are taken).  Each half is reloaded for the
+// next tile as soon as its MFMAs have taken it, and each K tile (float4 i of
+// thread t: key (t + 256 i) / (DK/4), dims 4 ((t + 256 i) % (DK/4))) is
+// loaded an iteration before it is written to LDS, so both prefetches cross
+// the loop's back edge and the compiler cannot sink them next to their use.
 template <int DK>
 __global__ __launch_bounds__(256) void flash_bwd_dq_ds_kernel(const float* __restrict__ K,
                                                               const float* __restrict__ dS, float* __restrict__ dQ,
                                                               int S, int H, int64_t ld, float scale, int nqb) {
   constexpr int NDB = DK / 32;
   constexpr int P = DK + 4;
+  constexpr int kPer = kBK * DK / 4 / 256;
   __shared__ __attribute__((aligned(16))) float sm[2 * kBK * P > 4 * 32 * (DK + 1) ? 2 * kBK * P : 4 * 32 * (DK + 1)];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int l32 = lane & 31, kh = lane >> 5;
@@ -662,34 +641,68 @@ __global__ __launch_bounds__(256) void flash_bwd_dq_ds_kernel(const float* __res
 #pragma unroll
     for (int v = 0; v < 16; v++) acc[d][v] = 0.f;
 
-  DsTile<DK> tile;
+  // native vectors: an array of HIP float4 carried across the loop stays in
+  // scratch memory, these stay in registers
+  fvec4 kt[kPer];
+  float4 dlo[4], dhi[4];
+  auto load_k = [&](int key0) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      kt[i] = *reinterpret_cast<const fvec4*>(K + (int64_t)(key0 + idx / (DK / 4)) * ld + hcol + (idx % (DK / 4)) * 4);
+    }
+  };
+  auto store_k = [&](float* __restrict__ ks) {
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+      const int idx = t + 256 * i;
+      *reinterpret_cast<fvec4*>(ks + (idx / (DK / 4)) * P + (idx % (DK / 4)) * 4) = kt[i];
+    }
+  };
+  auto load_d = [&](float4(&dd)[4], int key0) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) dd[j] = *reinterpret_cast<const float4*>(drow + key0 + 8 * j);
+  };
+  // the MFMAs of one 32-key half: step s pairs key 32 kb + 8 (s/4) + 4 kh + s%4
+  auto half = [&](const float* __restrict__ ks, float4(&dd)[4], int kb, int next) {
+    float dv[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float4 x = keep4(qin, dd[j]);
+      dv[4 * j] = x.x; dv[4 * j + 1] = x.y; dv[4 * j + 2] = x.z; dv[4 * j + 3] = x.w;
+    }
+    load_d(dd, next + 32 * kb);
+    __builtin_amdgcn_sched_barrier(0);  // issue the reload before the MFMAs
+#pragma unroll
+    for (int s2 = 0; s2 < 16; s2++) {
+      const int kr = kb * 32 + 8 * (s2 >> 2) + 4 * kh + (s2 & 3);
+#pragma unroll
+      for (int d = 0; d < NDB; d++)
+        acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[kr * P + d * 32 + l32], dv[s2], acc[d], 0, 0, 0);
+    }
+  };
+
   const int nkv = S / kBK;
-  tile.load(K, drow, ld, hcol, 0, qin, t);
-  tile.store_k(sm, t);
+  load_k(0);
+  store_k(sm);
+  // the loop's issue order (K tile, then the two halves), so that each wait
+  // in the loop covers only the loads it needs
+  load_k((nkv > 1 ? 1 : 0) * kBK);
+  load_d(dlo, 0);
+  load_d(dhi, 32);
   __syncthreads();
   for (int it = 0; it < nkv; it++) {
     const int cur = it & 1;
-    const bool more = it + 1 < nkv;
-    float dv[32];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      dv[4 * i] = tile.d[i].x; dv[4 * i + 1] = tile.d[i].y; dv[4 * i + 2] = tile.d[i].z; dv[4 * i + 3] = tile.d[i].w;
-    }
-    // unconditional (the last step reloads its own tile) so that the tile
-    // stays in registers
-    tile.load(K, drow, ld, hcol, (more ? it + 1 : it) * kBK, qin, t);
-  const float* ks = sm + cur * kBK * P;
-    // step s of key block kb pairs key 32kb + 8(s/4) + 4kh + s%4 = dv[16kb + s]
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int s2 = 0; s2 < 16; s2++) {
-        const int kr = kb * 32 + 8 * (s2 >> 2) + 4 * kh + (s2 & 3);
-#pragma unroll
-        for (int d = 0; d < NDB; d++)
-          acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ks[kr * P + d * 32 + l32], dv[16 * kb + s2], acc[d], 0, 0, 0);
-      }
-    tile.store_k(sm + (cur ^ 1) * kBK * P, t);
+    // K tile it+1 (loaded an iteration ago) into the buffer that the last
+    // iteration read; the barrier at this iteration's end publishes it.  The
+    // last iteration stores a tile that nothing reads.
+    store_k(sm + (cur ^ 1) * kBK * P);
+    load_k(min(it + 2, nkv - 1) * kBK);
+    __builtin_amdgcn_sched_barrier(0);
+    const int next = min(it + 1, nkv - 1) * kBK;  // the last step reloads its own tile
+    const float* ks = sm + cur * kBK * P;
+    half(ks, dlo, 0, next);
+    half(ks, dhi, 1, next);
     __syncthreads();
   }
   // dQ^T (d, query) -> LDS [query][d] -> rows of dQ
