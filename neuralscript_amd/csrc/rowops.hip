@@ -459,7 +459,16 @@ __global__ __launch_bounds__(1024) void exclusive_scan_kernel(const int* __restr
   const int64_t per = (n + 1023) / 1024;
   const int64_t b = t * per, e = b + per < n ? b + per : n;
   int s = 0;
-  for (int64_t i = b; i < e; i++) s += in[i];
+  if (per <= 8) {
+    // all of the chunk's loads in flight at once (n <= 8192)
+    int v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = b + k < e ? in[b + k] : 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) s += v[k];
+  } else {
+    for (int64_t i = b; i < e; i++) s += in[i];
+  }
   part[t] = s;
   __syncthreads();
   for (int o = 1; o < 1024; o <<= 1) {
@@ -491,16 +500,24 @@ __global__ __launch_bounds__(256) void emb_place_kernel(const float* __restrict_
   order[start[r] + pos] = (int)i;
 }
 
-// Sort the segments of rows [256*block, 256*block + 256).  Short segments
-// (<= 32 tokens) are insertion-sorted by their own thread; each longer one
-// is then ranked by the whole workgroup (rank = number of smaller token ids
-// in the segment, ids are distinct) through `tmp`.
+// Sort the segments of rows [256*block, 256*block + 256).  The block's
+// segment bounds are staged in LDS once.  Short segments (<= 32 tokens) are
+// insertion-sorted by their own thread; each longer one is listed and then
+// ranked by the whole workgroup (rank = number of smaller token ids in the
+// segment, ids are distinct) through `tmp`.
 __global__ __launch_bounds__(256) void emb_sort_segments_kernel(const int* __restrict__ start, int64_t V,
                                                                 int* __restrict__ order, int* __restrict__ tmp) {
+  __shared__ int st[257];
+  __shared__ int longrow[256];
+  __shared__ int nlong;
+  const int t = threadIdx.x;
   const int64_t r0 = (int64_t)blockIdx.x * 256;
-  const int64_t r = r0 + threadIdx.x;
-  if (r < V) {
-    const int b = start[r], e = start[r + 1];
+  const int nr = (int)(r0 + 256 < V ? 256 : V - r0);
+  if (t == 0) nlong = 0;
+  for (int i = t; i <= nr; i += 256) st[i] = start[r0 + i];
+  __syncthreads();
+  if (t < nr) {
+    const int b = st[t], e = st[t + 1];
     if (e - b <= 32) {
       for (int i = b + 1; i < e; i++) {
         const int v = order[i];
@@ -511,20 +528,22 @@ __global__ __launch_bounds__(256) void emb_sort_segments_kernel(const int* __res
         }
         order[j + 1] = v;
       }
+    } else {
+      longrow[atomicAdd(&nlong, 1)] = t;  // segments are disjoint: any listing order
     }
   }
-  const int64_t r1 = r0 + 256 < V ? r0 + 256 : V;
-  for (int64_t q = r0; q < r1; q++) {
-    const int b = start[q], e = start[q + 1];
-    if (e - b <= 32) continue;  // uniform across the workgroup
-    for (int i = b + (int)threadIdx.x; i < e; i += 256) {
+  __syncthreads();
+  const int nl = nlong;
+  for (int k = 0; k < nl; k++) {
+    const int b = st[longrow[k]], e = st[longrow[k] + 1];
+    for (int i = b + t; i < e; i += 256) {
       const int v = order[i];
       int rank = 0;
       for (int j = b; j < e; j++) rank += order[j] < v;
       tmp[b + rank] = v;
     }
     __syncthreads();
-    for (int i = b + (int)threadIdx.x; i < e; i += 256) order[i] = tmp[i];
+    for (int i = b + t; i < e; i += 256) order[i] = tmp[i];
     __syncthreads();
   }
 }
@@ -543,6 +562,51 @@ __global__ __launch_bounds__(256) void emb_grad_rows_kernel(const float* __restr
     float acc = 0.f;
     for (int t = b; t < e; t++) acc += dout[(int64_t)order[t] * D + c];
     o[c] = acc;
+  }
+}
+
+// The same sums for D % 4 == 0 on 16-byte aligned rows: NV float4 columns
+// per lane (256 NV columns per pass), the next token's rows loaded before
+// the current one is added, each column still summed in ascending token
+// order.
+template <int NV>
+__global__ __launch_bounds__(256) void emb_grad_rows_vec_kernel(const float* __restrict__ dout,
+                                                                const int* __restrict__ start,
+                                                                const int* __restrict__ order,
+                                                                float* __restrict__ dW, int64_t V, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= V) return;
+  const int b = start[r], e = start[r + 1];
+  const int64_t D4 = D / 4;
+  const float4* __restrict__ src = reinterpret_cast<const float4*>(dout);
+  float4* __restrict__ o = reinterpret_cast<float4*>(dW + r * D);
+  for (int64_t c0 = lane; c0 < D4; c0 += 64 * NV) {
+    float4 acc[NV], x[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) acc[j] = x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    int64_t row = b < e ? (int64_t)order[b] * D4 : 0;
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+      if (b < e && c0 + 64 * j < D4) x[j] = src[row + c0 + 64 * j];
+    for (int t = b; t < e; t++) {
+      float4 cur[NV];
+#pragma unroll
+      for (int j = 0; j < NV; j++) cur[j] = x[j];
+      if (t + 1 < e) {
+        row = (int64_t)order[t + 1] * D4;
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+          if (c0 + 64 * j < D4) x[j] = src[row + c0 + 64 * j];
+      }
+#pragma unroll
+      for (int j = 0; j < NV; j++) {
+        acc[j].x += cur[j].x; acc[j].y += cur[j].y; acc[j].z += cur[j].z; acc[j].w += cur[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+      if (c0 + 64 * j < D4) o[c0 + 64 * j] = acc[j];
   }
 }
 
@@ -584,8 +648,18 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
                        tmp);
     NSH_LAUNCHED();
   }
-  hipLaunchKernelGGL(emb_grad_rows_kernel, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, s, dout, start, order, dW,
-                     V, D);
+  const dim3 rg((unsigned)ceil_div(V, 4));
+  if (D % 4 == 0 && ((uintptr_t)dout | (uintptr_t)dW) % 16 == 0) {
+    const int64_t D4 = D / 4;
+    if (D4 >= 256)
+      hipLaunchKernelGGL(emb_grad_rows_vec_kernel<4>, rg, dim3(256), 0, s, dout, start, order, dW, V, D);
+    else if (D4 >= 128)
+      hipLaunchKernelGGL(emb_grad_rows_vec_kernel<2>, rg, dim3(256), 0, s, dout, start, order, dW, V, D);
+    else
+      hipLaunchKernelGGL(emb_grad_rows_vec_kernel<1>, rg, dim3(256), 0, s, dout, start, order, dW, V, D);
+  } else {
+    hipLaunchKernelGGL(emb_grad_rows_kernel, rg, dim3(256), 0, s, dout, start, order, dW, V, D);
+  }
   NSH_LAUNCHED();
   return 0;
 }

@@ -69,11 +69,21 @@ def test_activation_backward(act):
 
 
 @pytest.mark.parametrize("n,V,D,mode", [(16384, 8192, 512, "uniform"), (3000, 40, 16, "uniform"),
-                                        (700, 50, 33, "same"), (500, 1000, 8, "edge")])
+                                        (700, 50, 33, "same"), (500, 1000, 8, "edge"),
+                                        (4096, 64, 512, "same"), (20000, 300, 1024, "skew"),
+                                        (5000, 20000, 64, "uniform")])
 def test_embedding_grad_is_bit_exact(n, V, D, mode):
+    """Row sums in ascending token order: float4 columns (D % 4 == 0: one,
+    two or four float4 per lane) or scalar ones; short segments sorted per
+    thread, long ones (one row taking every token; several heavy rows in one
+    block under skewed ids) by the workgroup; V above 8192 takes the scan's
+    looping path."""
     print(f"embedding_grad n={n} V={V} D={D} {mode}", flush=True)
     if mode == "same":
         idx = np.full(n, 3.0, np.float32)   # one row takes every token
+    elif mode == "skew":
+        # a few rows take most tokens: segments of hundreds to thousands
+        idx = np.minimum(np.random.default_rng(13).pareto(1.1, n), V - 1).astype(np.int64).astype(np.float32)
     else:
         idx = synth.token_ids(11, n, V)
     if mode == "edge":
