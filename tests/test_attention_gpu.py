@@ -56,8 +56,9 @@ def core_bwd_ref(Q, K, V, dO, S, D, H):
     return dQ, dK, dV
 
 
-@pytest.mark.parametrize("S,D,H", [(64, 128, 2), (192, 128, 2), (100, 128, 2), (256, 64, 2), (130, 64, 2),
-                                   (90, 64, 8), (1024, 512, 8), (2048, 512, 8), (100, 128, 1), (77, 192, 2)])
+@pytest.mark.parametrize("S,D,H", [(64, 128, 2), (128, 128, 2), (192, 128, 2), (100, 128, 2), (256, 64, 2),
+                                   (130, 64, 2), (90, 64, 8), (1024, 512, 8), (2048, 512, 8), (100, 128, 1),
+                                   (77, 192, 2)])
 @pytest.mark.parametrize("store_ds", [0, 1])
 def test_attention_core_backward_matches_float64(S, D, H, store_ds):
     """Flash backward (head size 32/64: key-parallel dK/dV pass, then dQ
