@@ -8,16 +8,21 @@ oracle, which is pinned bitwise to the reference's emitted drivers):
   before it; the leading vectors with ratio > 1e-3 form the determined
   prefix), 4096 sampled entries of Q = (W0 - W1 - 0.01 lr W0) / (lr
   sqrt(min(r, c))) on that prefix and 4096 sampled gradient entries; plus
-  the step's loss.
+  the step's loss; (float64) the same gradient entries and loss evaluated in
+  float64 by oracle/f64.py, and the float64 MGS of the float64 gradient at
+  the sampled Q entries; (mgs_own) the float64 MGS of the oracle's own
+  gradient at the same entries.
 * c5a_full.npz -- the AdamW variant (c5a: `optimizer=adamw` on the step, a
   build knob, not reference-emitted), 10 steps at lr 3e-4: the losses, the
   per-matrix norms of W10 - W0, 65536 sampled entries of W10 and its digest;
-  and (adamw_sensitivity) the same 10 steps from 1-ulp-perturbed weights.
+  and (adamw_sensitivity) the same 10 steps from 1-ulp-perturbed weights;
+  (adamw_float64) the same 10 steps in float64 by oracle/f64.py.
 * curve_c5sa_206.npz -- the AdamW variant at the reduced c5 shape, 100 steps
   under the host's cosine-warmup lr: losses, weights after 20 and 100 steps,
   and the trajectory's own spread under 1-ulp weight noise.
 
-    OMP_NUM_THREADS=6 python tests/golden/make_c5_full_checks.py [update|sensitivity|adamw|adamw_sensitivity|curve]
+    OMP_NUM_THREADS=6 python tests/golden/make_c5_full_checks.py \
+        [update|sensitivity|float64|mgs_own|adamw|adamw_sensitivity|adamw_float64|curve]
 """
 import os
 import sys
@@ -142,6 +147,63 @@ def update():
     np.savez_compressed(os.path.join(HERE, "c5_full_update.npz"), **out)
 
 
+def float64():
+    """Adds to c5_full_update.npz the float64 evaluation of the same step's
+    gradients (oracle/f64.py: the reference's formulas in float64) at the
+    sampled entries (`<matrix>:g64`) and the float64 loss (`loss64`): the
+    yardstick against which the oracle's float32 rounding and the GPU's are
+    both measured."""
+    import f64
+    path = os.path.join(HERE, "c5_full_update.npz")
+    with np.load(path) as f:
+        out = {k: f[k] for k in f.files}
+    net, w0, x, y = setup("c5")
+    t0 = time.time()
+    vals, loss = f64.train_values(net, w0, x, y)
+    print(f"c5 float64 step: {time.time() - t0:.0f} s, loss {loss!r} (float32 oracle {float(out['loss'])!r})",
+          flush=True)
+    out["loss64"] = np.float64(loss)
+    for n_, r, c in net.weights:
+        g64 = vals[str(out[f"{n_}:grad"])]
+        out[f"{n_}:g64"] = g64[out[f"{n_}:gi"]].copy()
+        out[f"{n_}:g64rms"] = np.float64(np.sqrt(np.mean(g64 ** 2)))
+        # Q of the float64 gradient (MGS in float64) at the sampled entries,
+        # and the float64 gradient's own residual ratios
+        k = int(out[f"{n_}:k"])
+        q64, ratio64 = helpers.mgs64(g64, r, c, k)
+        out[f"{n_}:q64"] = q64[out[f"{n_}:vi"], out[f"{n_}:ei"]]
+        out[f"{n_}:ratio64"] = ratio64
+        d = np.abs(out[f"{n_}:g"].astype(np.float64) - out[f"{n_}:g64"])
+        print(f"  {n_}: oracle vs float64 max |d| / rms {d.max() / out[f'{n_}:g64rms']:.3g}, "
+              f"median {np.median(d) / out[f'{n_}:g64rms']:.3g}", flush=True)
+    np.savez_compressed(path, **out)
+
+
+def mgs_own():
+    """Adds to c5_full_update.npz the float64 MGS of the oracle's own
+    float32 gradients on their determined prefix, at the sampled entries
+    (`<matrix>:q64own`): the yardstick of the reference's Q, against which
+    the GPU test measures how far its own Q is from the float64 MGS of its
+    own gradient."""
+    path = os.path.join(HERE, "c5_full_update.npz")
+    with np.load(path) as f:
+        out = {k: f[k] for k in f.files}
+    net, w0, x, y = setup("c5")
+    rec = {}
+    t0 = time.time()
+    oracle.Model(net, w0).train_step(x, y, LR, rec)
+    print(f"c5 step: {time.time() - t0:.0f} s", flush=True)
+    for n_, r, c in net.weights:
+        G = rec["buf"][str(out[f"{n_}:grad"])]
+        assert np.array_equal(G[out[f"{n_}:gi"]], out[f"{n_}:g"]), "oracle drifted from the fixture"
+        q64own, ratio = helpers.own_mgs(G, n_, r, c, out)
+        out[f"{n_}:q64own"] = q64own
+        d = out[f"{n_}:q"] - q64own
+        print(f"  {n_}: reference Q vs float64 MGS of its gradient: rms {np.sqrt(np.mean(d ** 2)):.3g} "
+              f"max {np.max(np.abs(d)):.3g}", flush=True)
+    np.savez_compressed(path, **out)
+
+
 def adamw(steps=10):
     net, w0, x, y = setup("c5a")
     m = oracle.Model(net, w0)
@@ -160,6 +222,36 @@ def adamw(steps=10):
         out[f"{n_}:norm"] = np.float64(np.linalg.norm(m.w[o:o + r * c].astype(np.float64) - w0[o:o + r * c]))
     np.savez_compressed(os.path.join(HERE, "c5a_full.npz"), **out)
 
+
+
+def adamw_float64():
+    """Adds to c5a_full.npz the same 10 AdamW steps evaluated in float64
+    (oracle/f64.py: gradients and updates by the reference's formulas) at
+    the sampled weights (`w64_sample`) and its losses (`losses64`)."""
+    import f64
+    path = os.path.join(HERE, "c5a_full.npz")
+    with np.load(path) as f:
+        out = {k: f[k] for k in f.files}
+    net, w0, x, y = setup("c5a")
+    w = w0.astype(np.float64)
+    state = {n_: (np.zeros(r * c), np.zeros(r * c)) for n_, r, c in net.weights}
+    grads = {}
+    for ins in net.train.instrs:
+        if ins.op == "ns.opt.step":
+            grads = {ins.operands[k]: ins.operands[k + 1] for k in range(0, len(ins.operands) - 1, 2)}
+    losses = []
+    for s in range(int(out["steps"])):
+        t0 = time.time()
+        vals, loss = f64.train_values(net, w, x, y)
+        losses.append(loss)
+        for n_, r, c in net.weights:
+            o = net.offsets[n_]
+            m, v = state[n_]
+            f64.adamw_step(w[o:o + r * c], vals[grads[n_]], m, v, s + 1, float(out["lr"]))
+        print(f"float64 c5a step {s}: loss {loss:.7f} ({time.time() - t0:.0f} s)", flush=True)
+    out["losses64"] = np.array(losses, np.float64)
+    out["w64_sample"] = w[out["idx"]].copy()
+    np.savez_compressed(path, **out)
 
 
 def adamw_sensitivity(seed=8):
@@ -229,7 +321,9 @@ def adamw_curve(rows=256, seed=206, base=1e-3, trials=4):
           f"steps {s20:.3g}, after 100 {s100:.3g}", flush=True)
 
 if __name__ == "__main__":
-    what = sys.argv[1:] or ["update", "sensitivity", "adamw", "adamw_sensitivity", "curve"]
+    what = sys.argv[1:] or ["update", "sensitivity", "float64", "mgs_own", "adamw", "adamw_sensitivity",
+                            "adamw_float64", "curve"]
     for wname in what:
-        {"update": update, "sensitivity": update_sensitivity, "adamw": adamw, "adamw_sensitivity": adamw_sensitivity,
+        {"update": update, "sensitivity": update_sensitivity, "float64": float64, "mgs_own": mgs_own,
+         "adamw": adamw, "adamw_sensitivity": adamw_sensitivity, "adamw_float64": adamw_float64,
          "curve": adamw_curve}[wname]()

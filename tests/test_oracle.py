@@ -414,7 +414,8 @@ def test_full_size_muon_update_check_rejects_broken_optimizers():
     with a no-op optimizer (W1 = W0) and with lr x 2 (the gradient at W0 does
     not depend on lr, so that run's update is exactly twice this one's, up
     to the decay term, which is computed here): both fail on every matrix
-    by the update's norm."""
+    by the update's norm; a Q three times as far from the float64 MGS as
+    the reference's fails on every matrix by Q."""
     from neuralscript_amd import workloads
     g = load_golden("c5_full_update")
     net = oracle.Net(helpers.ir_text("c5"))
@@ -433,34 +434,119 @@ def test_full_size_muon_update_check_rejects_broken_optimizers():
         own[n] = (norm, q)
         noop[n] = (0.0, -decay)
         double[n] = (2.0 * norm, 2.0 * q + decay)
-    assert not helpers.muon_update_failures(own, g, helpers.C5_Q_ATOL)
+    # the reference's own gradient's float64 MGS (its Q's yardstick)
+    ref_own = {n: (g[n + ":q64own"], g[n + ":ratio"][g[n + ":vi"]]) for n in own}
+    assert not helpers.muon_update_failures(own, g, ref_own)
     for broken in (noop, double):
-        fails = helpers.muon_update_failures(broken, g, helpers.C5_Q_ATOL)
+        fails = helpers.muon_update_failures(broken, g, ref_own)
         assert {f.split(":")[0] for f in fails if "|dW|" in f} == set(own), fails
+    # Q moved away from the float64 MGS -- twice as far again as the
+    # reference's own Q where its distance sets the bound, by 10x the rms
+    # floor where the reference is closer than the floor: the Q check fails
+    # on every matrix (by rms), the norm check on none
+    rng = np.random.default_rng(3)
+    far = {}
+    for n, (norm, q) in own.items():
+        q64, ratio = ref_own[n]
+        sel = ratio >= helpers.MUON_Q_RATIO
+        scale = float(np.sqrt(np.mean(q64[sel] ** 2)))
+        if np.sqrt(np.mean((q - q64)[sel] ** 2)) >= helpers.MUON_Q_FLOOR_RMS * scale:
+            far[n] = (norm, q + 2.0 * (q - q64))
+        else:
+            far[n] = (norm, q64 + 10 * helpers.MUON_Q_FLOOR_RMS * scale * rng.choice([-1.0, 1.0], q.size))
+    fails = helpers.muon_update_failures(far, g, ref_own)
+    assert {f.split(":")[0] for f in fails if "rms |Q" in f} == set(own), fails
+    assert not [f for f in fails if "|dW|" in f]
 
 
 @pytest.mark.skipif(not os.path.exists(os.path.join(helpers.GOLDEN, "c5a_full.npz")),
                     reason="full-size AdamW fixture not written")
+def test_full_size_gradient_check_rejects_scaled_and_broken_gradients():
+    """The float64 assertion of test_c5_full_size_first_muon_update_matches_
+    oracle (helpers.full_gradient_failures) accepts the reference's own
+    gradients (the oracle's, bit-identical to it) and the float64 values
+    rounded to float32, and rejects on every one of the eight matrices the
+    reference's gradient scaled by 1.001, the rounded float64 gradient
+    scaled by 1.001 or 0.999, the gradient with noise of twice the
+    reference's own error added, and a zero gradient.  (The reference's own
+    gradient scaled by 0.999 is not rejected everywhere: on two matrices its
+    own scale error is +7e-4, and 0.999 moves it towards 1.)"""
+    g = load_golden("c5_full_update")
+    names = [n for n, _, _ in oracle.Net(helpers.ir_text("c5")).weights]
+    own = {n: g[n + ":g"] for n in names}
+    exact = {n: g[n + ":g64"].astype(np.float32) for n in names}
+    assert not helpers.full_gradient_failures(own, g)
+    assert not helpers.full_gradient_failures(exact, g)
+    rng = np.random.default_rng(5)
+    broken = {
+        "x1.001": {n: own[n] * np.float32(1.001) for n in names},
+        "exact x1.001": {n: exact[n] * np.float32(1.001) for n in names},
+        "exact x0.999": {n: exact[n] * np.float32(0.999) for n in names},
+        "noise": {n: (g[n + ":g64"] + 2.0 * rng.permutation(own[n] - g[n + ":g64"])).astype(np.float32)
+                  for n in names},
+        "zero": {n: np.zeros_like(own[n]) for n in names},
+    }
+    for kind, samples in broken.items():
+        fails = helpers.full_gradient_failures(samples, g)
+        assert {f.split(" ")[0] for f in fails} == set(names), (kind, fails)
+
+
+def test_float64_evaluation_agrees_with_the_oracle_on_small_networks():
+    """oracle/f64.py, the float64 yardstick, evaluates the reference's
+    formulas: on small networks (where float32 rounding is tiny) every value
+    of a training step's forward and reverse bodies agrees with the
+    bit-exact float32 oracle to 1e-5 of its largest magnitude (a dropped
+    term, a wrong sign or a transposed operand moves values by O(1) of it),
+    and the loss to 1e-6."""
+    import f64
+    for name, rows in (("c5s", 64), ("c5h", 100), ("mlpt", 17), ("c5t", 40), ("moet", None)):
+        if rows is None:
+            with pytest.raises(NotImplementedError):
+                net = oracle.Net(helpers.ir_text(name))
+                f64.train_values(net, helpers.net_weights(name, 1), helpers.net_inputs(net, name, 1, 8),
+                                 helpers.net_labels(net, 1, 8))
+            continue
+        net = oracle.Net(helpers.ir_text(name))
+        seed = 400 + rows
+        x = helpers.net_inputs(net, name, seed, rows)
+        y = helpers.net_labels(net, seed, rows)
+        w = helpers.net_weights(name, seed)
+        rec = {}
+        loss = oracle.Model(net, w).train_step(x, y, 0.02, rec)
+        vals, loss64 = f64.train_values(net, w, x, y)
+        assert abs(loss64 - float(loss)) <= 1e-6 * max(1.0, abs(loss64)), name
+        checked = 0
+        for k, v in vals.items():
+            if k in rec["buf"]:
+                ref = rec["buf"][k].astype(np.float64)
+                scale = max(float(np.max(np.abs(v))), 1e-30)
+                assert np.max(np.abs(ref - v)) <= 1e-5 * scale, (name, k, np.max(np.abs(ref - v)) / scale)
+                checked += 1
+        assert checked >= 8, (name, checked)
+
+
 def test_full_size_adamw_weight_check_separates_rounding_from_broken_steps():
     """The sampled-weight assertion of test_c5_full_size_adamw_variant_ten_steps
-    (at least half of the samples within the fp32 bar) accepts the oracle's
-    own 10 steps from 1-ulp-perturbed weights (fixture `ulp_within`) and
-    rejects a no-op optimizer, a doubled lr and lr x 1.1 (their weights,
-    to first order W0 + k (W10 - W0) for k = 0, 2, 1.1)."""
+    (helpers.adamw_f64_failures: at least as accurate as the reference
+    against the float64 trajectory) accepts the reference's own weights and
+    the float64 weights rounded to float32, and rejects a no-op optimizer, a
+    doubled lr, lr x 1.1 and lr x 0.5 (their weights, to first order W0 +
+    k (W10 - W0) for k = 0, 2, 1.1, 0.5) and the reference's weights with
+    noise of twice their own distance to float64 added."""
     from neuralscript_amd import workloads
     g = load_golden("c5a_full")
     net = oracle.Net(helpers.ir_text("c5a"))
     layout = [(n, net.offsets[n], r * c) for n, r, c in net.weights]
     w0 = workloads.weights("c5", layout, workloads.ir_shapes(helpers.ir_text("c5a")))
     wr = g["w_sample"].astype(np.float64)
+    w64 = g["w64_sample"]
     d = wr - w0[g["idx"]].astype(np.float64)
-
-    def within(w):
-        return float(np.mean(np.abs(w - wr) <= 1e-5 + 1e-4 * np.abs(wr)))
-
-    assert float(g["ulp_within"]) >= 0.5
+    assert not helpers.adamw_f64_failures(wr, g)
+    assert not helpers.adamw_f64_failures(w64.astype(np.float32), g)
     for k in (0.0, 2.0, 1.1, 0.5):
-        assert within(wr + (k - 1.0) * d) < 0.5, k
+        assert helpers.adamw_f64_failures(wr + (k - 1.0) * d, g), k
+    noisy = w64 + 2.0 * np.random.default_rng(9).permutation(wr - w64)
+    assert helpers.adamw_f64_failures(noisy, g)
 
 
 def test_reference_order_attention_sampling_hook_matches_the_checker():

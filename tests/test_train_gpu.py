@@ -142,14 +142,16 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     the device by IR value name) against the oracle's value of the same
     name; the weights after the optimizer last.
 
-    A value passes at the north star's bar, |d| <= 1e-5 + 1e-4 |ref|, or
-    within 4x the movement that a random 1-ulp perturbation of the weights
-    causes in the reference itself, measured at the same bar (its
-    conditioning).  The second bound matters only where the
-    network amplifies rounding: at 2048 tokens the attention output is an
-    average over 2048 rows (rms 0.025) that LayerNorm rescales by ~40, so the
-    reference's own logits move by 1.6x the first bound under 1-ulp weight
-    noise."""
+    A value passes at the north star's bar, |d| <= 1e-5 + 1e-4 |ref|, or,
+    where the network amplifies rounding beyond it, by being at least half
+    as accurate as the reference itself against the same formulas evaluated
+    in float64 (oracle/f64.py; violations at the same bar): at 2048 tokens
+    the attention output is an average over 2048 rows (rms 0.025) that
+    LayerNorm rescales by ~40, so the reference's own float32 logits sit
+    beyond the bar from the float64 ones.  Networks with operations the
+    float64 evaluation does not cover (softmax, dropout, MoE) fall back to
+    4x the movement that a random 1-ulp perturbation of the weights causes
+    in the reference, measured at the same bar."""
     ir = helpers.ir_text(name)
     net = oracle.Net(ir)
     seed = 400 + rows
@@ -163,6 +165,11 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     wp = (w * (1 + np.float32(2.0 ** -23) * rng.choice(np.array([-1, 1], np.float32), w.size))).astype(np.float32)
     rec_p = {}
     oracle.Model(net, wp).train_step(x, y, 0.02, rec_p)
+    import f64
+    try:
+        vals64, _ = f64.train_values(net, w, x, y)
+    except NotImplementedError:
+        vals64 = None
     model = runtime.Model(runtime.Plan(ir), w)
     model.train_step(x, y, 0.02)
     bad = []
@@ -185,6 +192,14 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
         ref = rec["buf"][v]
         got = model.read_value(v, ref.size)
         viol = helpers.violation(got, ref)
+        if vals64 is not None and v in vals64:
+            # at least half as accurate as the reference against float64
+            v64, o64 = helpers.violation(got, vals64[v]), helpers.violation(ref, vals64[v])
+            print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g}; vs float64 x{v64:.3g} "
+                  f"(the reference x{o64:.3g})")
+            if viol > 1.0 and v64 > max(1.0, 2.0 * o64):
+                bad.append((ins.op, v, viol, v64, o64))
+            continue
         floor = helpers.violation(rec_p["buf"][v], ref)
         print(f"  {ins.op:24s} {v:8s} n={ref.size:7d} violation x{viol:.3g} (1-ulp weight noise: x{floor:.3g})")
         if viol > max(1.0, 4.0 * floor):
@@ -312,18 +327,22 @@ def _c5_full(name):
 
 def test_c5_full_size_first_muon_update_matches_oracle():
     """Config c5 at full size, one training step at lr 3e-4 from the seeded
-    weights, against the oracle: per matrix, the update's Frobenius norm
-    within 1e-3 (it is lr * min(r, c) for any summation order, so a no-op
-    optimizer, a doubled lr or a wrong sqrt(min(r, c)) factor fail); the Q
-    entries sampled on the gradient's determined prefix within
-    helpers.muon_q_tolerance (at 16384 tokens the attention averages nearly
-    identical rows that LayerNorm rescales, so the reference itself moves
-    far more than fp32 rounding: the fixture records how much under 1-ulp
-    weight noise); the step's loss (a pure forward) within the fp32 bar.
-    The sampled gradient entries are reported beside the oracle's own 1-ulp
-    movement: at this size their non-dominant components are set by that
-    conditioning (the gradients are nearly rank one, and the dominant
-    direction, Q's first vector, agrees to 1e-5)."""
+    weights.  At 16384 tokens the forward is ill-conditioned (the attention
+    averages nearly identical rows that LayerNorm rescales), so the
+    reference's own float32 gradients are off by up to a few % of their rms
+    from the same formulas evaluated in float64 (tests/golden/
+    make_c5_full_checks.py float64; oracle/f64.py).  Against those float64
+    values every one of the eight sampled gradients must be at least as
+    accurate as the reference's (rms and max error, and a least-squares
+    scale error within max(2e-4, the reference's): a gradient scaled by
+    1.001 fails, test_full_size_gradient_check_rejects_scaled_and_broken_
+    gradients).  The update: its Frobenius norm within 1e-3 of the oracle's
+    (lr * min(r, c) for any summation order, so a no-op optimizer, a doubled
+    lr or a wrong sqrt(min(r, c)) factor fail) and Q, on the vectors that
+    keep >= 5% of their norm in Gram-Schmidt, at least as close (rms, max)
+    to the float64 MGS of the GPU's own gradient as the reference's Q is to
+    the float64 MGS of the reference's gradient.  The step's loss (a pure
+    forward) within the fp32 bar of the oracle's."""
     g = np.load(os.path.join(helpers.GOLDEN, "c5_full_update.npz"))
     plan, net, w, x, y, digest = _c5_full("c5")
     assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w_digest"]), "input generator drifted"
@@ -332,20 +351,24 @@ def test_c5_full_size_first_muon_update_matches_oracle():
     dx, dy = runtime.DeviceArray.from_host(x), runtime.DeviceArray.from_host(y)
     loss = model.train_step_device(dx, dy, float(g["lr"]))
     w1 = model.get_weights()
-    grads = {n: model.read_value(str(g[n + ":grad"]), r * c) for n, r, c in net.weights}
+    full = {n: model.read_value(str(g[n + ":grad"]), r * c) for n, r, c in net.weights}
     model.free()
+    grads = {n: full[n][g[n + ":gi"]] for n in full}
+    own = {n: helpers.own_mgs(full[n], n, r, c, g) for n, r, c in net.weights}
     stats = helpers.muon_update_stats(w, w1, float(g["lr"]), net.weights, net.offsets, g)
-    fails = helpers.muon_update_failures(stats, g, helpers.C5_Q_ATOL)
+    fails = helpers.muon_update_failures(stats, g, own) + helpers.full_gradient_failures(grads, g)
+    print(f"  loss {loss:.7f} (oracle {float(g['loss']):.7f}, float64 {float(g['loss64']):.7f})")
     for name, (norm, q) in stats.items():
-        dq = float(np.max(np.abs(q - g[name + ":q"])))
-        rms = float(g[name + ":grms"])
-        gs, gr = grads[name][g[name + ":gi"]], g[name + ":g"]
-        viol = helpers.violation(gs, gr, atol=1e-5 * rms, rtol=1e-4)
-        floor = helpers.violation(g[name + ":g_ulp"], gr, atol=1e-5 * rms, rtol=1e-4)
-        print(f"  {name}: |dW| {norm:.6g} (oracle {float(g[name + ':norm']):.6g}); determined "
-              f"{int(g[name + ':k'])} vectors, max |dQ| {dq:.3g} (tolerance "
-              f"{helpers.muon_q_tolerance(g, name, helpers.C5_Q_ATOL):.3g}); gradient violation x{viol:.3g} "
-              f"(1-ulp weight noise: x{floor:.3g})")
+        a = helpers.accuracy_vs_f64(grads[name], g[name + ":g64"])
+        o = helpers.accuracy_vs_f64(g[name + ":g"], g[name + ":g64"])
+        b_rms, b_max = helpers.muon_q_bounds(g, name)
+        sel = own[name][1] >= helpers.MUON_Q_RATIO
+        dq = np.asarray(q, np.float64)[sel] - own[name][0][sel]
+        print(f"  {name}: gradient vs float64 rms {a['rms']:.3g} max {a['max']:.3g} scale {a['scale']:+.2g} "
+              f"(reference rms {o['rms']:.3g} max {o['max']:.3g} scale {o['scale']:+.2g}); |dW| {norm:.6g} "
+              f"(oracle {float(g[name + ':norm']):.6g}); Q vs float64 MGS of its gradient on {int(sel.sum())} "
+              f"samples rms {np.sqrt(np.mean(dq ** 2)):.3g} max {np.max(np.abs(dq)):.3g} (bounds {b_rms:.3g}, "
+              f"{b_max:.3g}); vs the float64 gradient's MGS max {np.max(np.abs(q - g[name + ':q64'])[sel]):.3g}")
     helpers.assert_close(np.float32(loss), g["loss"], "c5 first loss")
     assert not fails, fails
 
@@ -355,15 +378,17 @@ def test_c5_full_size_adamw_variant_ten_steps():
     at full size: 10 steps at lr 3e-4 against the oracle -- every loss within
     plain 1e-3 (the curve falls 0.21 over the 10 steps, so a no-op optimizer
     or a doubled lr fails), the per-matrix norm of W10 - W0 within 2%, and
-    at least half of the 65536 sampled weights within the fp32 bar.  AdamW
-    turns a gradient element that cancels to ~0 into a +-lr step whose sign
-    follows rounding, and at this sequence length the gradients themselves
-    are ill-conditioned (see the first-update test): the oracle's own steps
-    from weights perturbed by one ulp keep 95.9% of the samples within the
-    bar (fixture `ulp_within`), a different summation order in every
-    reduction (the GPU's) keeps about 77%, while a wrong step size leaves
-    only the weights whose 10-step update is itself below the bar: 11% for
-    no step or a doubled lr, 15% for lr x 1.1 (checked here as `noop`)."""
+    the 65536 sampled weights at least as accurate as the reference's against
+    the same 10 steps evaluated in float64 (oracle/f64.py; helpers.
+    adamw_f64_failures): as large a fraction within the fp32 bar and no
+    larger an rms distance.  AdamW turns a gradient element that cancels to
+    ~0 into a +-lr step whose sign follows rounding, and at this sequence
+    length the gradients themselves are ill-conditioned (see the
+    first-update test): the reference's own float32 run keeps only ~77% of
+    the samples within the bar of the float64 one, while a wrong step size
+    leaves only the weights whose 10-step update is itself below the bar:
+    11% for no step or a doubled lr, 15% for lr x 1.1 (checked here as
+    `noop`)."""
     g = np.load(os.path.join(helpers.GOLDEN, "c5a_full.npz"))
     plan, net, w, x, y, digest = _c5_full("c5a")
     assert digest(x) == str(g["x_digest"]) and digest(w) == str(g["w0_digest"]), "input generator drifted"
@@ -377,9 +402,13 @@ def test_c5_full_size_adamw_variant_ten_steps():
     ws, wr = w10[g["idx"]].astype(np.float64), g["w_sample"].astype(np.float64)
     within = float(np.mean(np.abs(ws - wr) <= 1e-5 + 1e-4 * np.abs(wr)))
     noop = float(np.mean(np.abs(w[g["idx"]].astype(np.float64) - wr) <= 1e-5 + 1e-4 * np.abs(wr)))
+    a64, o64 = helpers.adamw_f64_stats(ws, g), helpers.adamw_f64_stats(wr, g)
     print(f"  losses {losses[0]:.6f} .. {losses[-1]:.6f}; max |loss - oracle| {dev.max():.3g}; sampled weights "
-          f"within the fp32 bar: {100 * within:.2f}% (oracle under 1-ulp noise {100 * float(g['ulp_within']):.2f}%,"
-          f" no optimizer step {100 * noop:.2f}%), max |d| {np.max(np.abs(ws - wr)):.3g}")
+          f"within the fp32 bar of the oracle's: {100 * within:.2f}% (no optimizer step {100 * noop:.2f}%), "
+          f"max |d| {np.max(np.abs(ws - wr)):.3g}; against the float64 trajectory: within the bar "
+          f"{100 * a64['within']:.2f}%, rms |d| {a64['rms']:.3g} (the reference: {100 * o64['within']:.2f}%, "
+          f"{o64['rms']:.3g})")
+    fails = helpers.adamw_f64_failures(ws, g)
     norms = []
     for name, r, c in net.weights:
         o = net.offsets[name]
@@ -388,6 +417,6 @@ def test_c5_full_size_adamw_variant_ten_steps():
     print("  |W10 - W0| vs oracle:", [(a, round(b / c, 5)) for a, b, c in norms])
     assert np.all(dev <= LOSS_TOL), dev
     assert noop < 0.2, noop
-    assert within >= 0.5, (within, noop)
+    assert not fails, fails
     for name, n, ref in norms:
         assert abs(n - ref) <= 0.02 * ref, (name, n, ref)
