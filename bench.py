@@ -93,24 +93,34 @@ def c5_work(M=16384, D=512, FF=2048, C=8192):
             "total": 3 * dense_fwd + 12.0 * M * M * D}
 
 
-def c5_hbm_bytes(n_muon, M=16384, D=512, C=8192):
+def c5_hbm_bytes(n_muon, M=16384, D=512, C=8192, V=8192):
     """Algorithmic HBM bytes per step of c5's bandwidth-bound regions: CE reads
     the logits and the one-hot labels and writes the gradient ([M, C] each);
     the Muon gather reads g and writes its transpose, the update reads the q
     vectors and w and writes w (n_muon elements each); embedding and LayerNorm
-    read and write [M, D] (LayerNorm's gradient also reads x)."""
+    read and write [M, D] (LayerNorm's gradient also reads x); the embedding
+    gradient as emb_grad_bytes."""
     return {"softmax_xent": 3.0 * M * C * 4, "muon_gather": 2.0 * n_muon * 4, "muon_update": 3.0 * n_muon * 4,
-            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4}
+            "embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4,
+            "embedding_grad": emb_grad_bytes(M, V, D)}
 
 
-HBM_REGIONS = ("embedding", "layernorm", "layernorm_grad", "softmax_xent", "muon_gather", "muon_update")
+def emb_grad_bytes(M, V, D):
+    """The embedding gradient reads the [M, D] gradient rows and the M ids
+    and writes the whole [V, D] table once."""
+    return (M * D + M + V * D) * 4.0
+
+
+HBM_REGIONS = ("embedding", "layernorm", "layernorm_grad", "softmax_xent", "muon_gather", "muon_update",
+               "embedding_grad")
 
 # Dominant kernel of each config: (profile region, kernel name, bound).
 DOMINANT = {"c2": ("gemm", "gemm_f32_kernel", "mfma"),
             "c3": ("attention_fwd", "flash_fwd_kernel<64>", "mfma"),
+            "c3d": ("attention_fwd", "flash_fwd_kernel<128>", "mfma"),
             "c4": ("moe_experts", "gemm_f32_kernel (grouped by expert, gather/scatter rows)", "mfma"),
             "c5": ("attention_bwd", "flash_bwd_dkdv_kernel<64,true> + flash_bwd_dq_ds_kernel<64>", "mfma")}
-TRAFFIC_KEY = {"c2": "gemm_f32_kernel", "c3": "c3:attention_fwd", "c4": "c4:moe_experts",
+TRAFFIC_KEY = {"c2": "gemm_f32_kernel", "c3": "c3:attention_fwd", "c3d": "c3d:attention_fwd", "c4": "c4:moe_experts",
                "c5": "c5:attention_bwd"}
 
 
@@ -222,7 +232,7 @@ def bench_forward(key, steps, warmup, with_cpu, budget):
     model.free()
     dx.free()
     dy.free()
-    work = {"c2": c2_work, "c3": c3_work, "c4": c4_work}[key]()
+    work = {"c2": c2_work, "c3": c3_work, "c3d": c3_work, "c4": c4_work}[key]()
     hbm = {k: v for k, v in work.items() if k in HBM_REGIONS}
     res = {"value": wl.rows * steps / dt, "unit": "tokens/s", "ms_per_step": dt * 1e3 / steps,
            "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device",
@@ -231,7 +241,7 @@ def bench_forward(key, steps, warmup, with_cpu, budget):
                         "note": "ns_eval_infer with host buffers (PCIe-inclusive)"}}
     if routing is not None:
         res["routing"] = routing
-    if with_cpu:
+    if with_cpu and key != "c3d":  # c3d is no BASELINE config: no CPU leg
         res["cpu_baseline"] = {"c2": cpu_c2, "c3": cpu_c3, "c4": cpu_c4}[key](w, budget)
     return res
 
@@ -273,6 +283,23 @@ def adamw_bandwidth(n, launches=20):
             "note": "the whole parameter count of the step through the AdamW kernel (28 B per parameter)"}
 
 
+def rowop_bandwidth(dx, dy, M=16384, D=512, V=8192, C=8192, reps=50):
+    """The step's row kernels at c5's shapes (its own ids and labels), each
+    timed over `reps` back-to-back launches (nsh_bench_rowops): for kernels of
+    10-50 us the per-launch HIP events of the profile regions add a large
+    share of their time."""
+    from neuralscript_amd import runtime
+    us = (ctypes.c_double * 5)()
+    runtime.check(runtime.lib().nsh_bench_rowops(dx.ptr, dy.ptr, M, D, V, C, reps, us), "bench_rowops")
+    nbytes = {"embedding": 2.0 * M * D * 4, "layernorm": 2.0 * M * D * 4, "layernorm_grad": 3.0 * M * D * 4,
+              "embedding_grad": emb_grad_bytes(M, V, D), "softmax_xent": 3.0 * M * C * 4}
+    out = {"note": f"each kernel over {reps} back-to-back launches at c5's shapes, one event pair"}
+    for k, (name, b) in enumerate(nbytes.items()):
+        gbs = b / (us[k] * 1e-6) / 1e9
+        out[name] = {"us_per_launch": us[k], "bytes": b, "GB/s": gbs, "hbm_frac": gbs / HBM_PEAK_GBS}
+    return out
+
+
 def bench_train(key, steps, warmup, with_cpu, budget):
     """Device-resident training steps (nsh_train_step_device); lr = 3e-4
     times the cosine-warmup multiplier, as the host applies it."""
@@ -298,6 +325,7 @@ def bench_train(key, steps, warmup, with_cpu, budget):
         t[0] += 1
     abi_dt = (time.perf_counter() - t0) / 2
     model.free()
+    row_kernels = rowop_bandwidth(dx, dy) if key == "c5" else None
     dx.free()
     dy.free()
     work = c5_work()
@@ -308,7 +336,7 @@ def bench_train(key, steps, warmup, with_cpu, budget):
            "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device",
            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
            "roofline": roofline_of(key, work, prof), "kernels": kernel_table(prof, steps, work, c5_hbm_bytes(n_muon)),
-           "adamw": adamw_bandwidth(n_muon),
+           "adamw": adamw_bandwidth(n_muon), "row_kernels": row_kernels,
            "host_abi": {"steps_per_s": 1.0 / abi_dt, "ms": abi_dt * 1e3,
                         "note": "ns_runtime_train_step with host buffers (labels uploaded every call)"}}
     if with_cpu:
@@ -552,24 +580,33 @@ def cpu_c5(w, budget=20.0, m_small=64, nq=8, nk=8):
 # peaks and calibration
 # ---------------------------------------------------------------------------
 
-def measured_peaks():
-    """Attainable peaks of this GPU, measured by libnship's microbenchmarks:
-    a register-only fp32 MFMA loop (2048 workgroups x 4 waves, 4 independent
-    32x32x2 chains per wave) and a float4 copy of 256 MiB each way."""
+def measured_peaks(reps=3):
+    """Attainable peaks of this GPU, measured by libnship's microbenchmarks,
+    best of `reps` runs each: a register-only fp32 MFMA loop (2048 workgroups
+    x 4 waves, 4 independent 32x32x2 chains per wave) and a float4 copy of
+    256 MiB each way.  The default run measures them first, on a cold GPU
+    (the MFMA clock falls as the GPU heats)."""
     from neuralscript_amd import runtime
     lib = runtime.lib()
     tf = ctypes.c_double()
-    runtime.check(lib.nsh_bench_mfma_peak(4000, 2048, ctypes.byref(tf)), "bench_mfma_peak")
+    tfs = []
+    for _ in range(reps):
+        runtime.check(lib.nsh_bench_mfma_peak(4000, 2048, ctypes.byref(tf)), "bench_mfma_peak")
+        tfs.append(tf.value)
     n = 1 << 26
     src, dst = runtime.DeviceArray(n), runtime.DeviceArray(n)
     src.fill_zero()
     dst.fill_zero()
     gbs = ctypes.c_double()
-    runtime.check(lib.nsh_bench_copy(src.ptr, dst.ptr, n, 10, ctypes.byref(gbs)), "bench_copy")
+    bws = []
+    for _ in range(reps):
+        runtime.check(lib.nsh_bench_copy(src.ptr, dst.ptr, n, 10, ctypes.byref(gbs)), "bench_copy")
+        bws.append(gbs.value)
     src.free()
     dst.free()
-    return {"mfma_f32_tflops": tf.value, "mfma_frac_of_published": tf.value / MFMA_F32_PEAK_TFLOPS,
-            "hbm_copy_gbs": gbs.value, "hbm_frac_of_published": gbs.value / HBM_PEAK_GBS}
+    return {"mfma_f32_tflops": max(tfs), "mfma_frac_of_published": max(tfs) / MFMA_F32_PEAK_TFLOPS,
+            "hbm_copy_gbs": max(bws), "hbm_frac_of_published": max(bws) / HBM_PEAK_GBS,
+            "runs": {"mfma_f32_tflops": tfs, "hbm_copy_gbs": bws}}
 
 
 def library_gemm(M=8192, N=4096, K=4096, reps=20):
@@ -650,10 +687,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="all", choices=["all", "c2", "c3", "c4", "c5", "moe_bwd", "copy", "peak"],
-                    help="all (default): c5 training steps/s as the headline, c2/c3/c4 forward nested under "
-                         "`configs`; c2..c5 alone (profiling runs); copy: the rocprof counter calibration "
-                         "copy; peak: attainable MFMA / HBM peaks and the vendor library's fp32 GEMM")
+    ap.add_argument("--config", default="all",
+                    choices=["all", "c2", "c3", "c3d", "c4", "c5", "moe_bwd", "copy", "peak"],
+                    help="all (default): c5 training steps/s as the headline, c2/c3/c4 forward (and c3d: c3 "
+                         "with 8 heads of 128) nested under `configs`; c2..c5 alone (profiling runs); copy: "
+                         "the rocprof counter calibration copy; peak: attainable MFMA / HBM peaks and the "
+                         "vendor library's fp32 GEMM")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=8.0,
                     help="seconds of single-core CPU work per sampled baseline leg")
@@ -670,17 +709,18 @@ def main():
         res = headline(bench_train("c5", a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
     elif a.config == "moe_bwd":
         res = bench_moe_backward(a.steps, a.warmup)
-    elif a.config in ("c2", "c3", "c4"):
+    elif a.config in ("c2", "c3", "c3d", "c4"):
         res = headline(bench_forward(a.config, a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
     else:
+        peaks = measured_peaks()
         res = headline(bench_train("c5", a.steps, a.warmup, cpu, a.cpu_budget), a.steps, a.warmup)
         res["configs"] = {}
-        for key in ("c2", "c3", "c4"):
+        for key in ("c2", "c3", "c3d", "c4"):
             print(f"bench.py: {key}", file=sys.stderr, flush=True)
             res["configs"][key] = bench_forward(key, a.steps, a.warmup, cpu, a.cpu_budget)
         print("bench.py: MoE backward at production shape", file=sys.stderr, flush=True)
         res["moe_backward"] = bench_moe_backward(min(a.steps, 10), min(a.warmup, 2))
-        res["measured_peak"] = measured_peaks()
+        res["measured_peak"] = peaks
         res["host"] = host_info()
     print(json.dumps(res), flush=True)
 

@@ -48,6 +48,7 @@ int nsh_device_count(void);
 /* Device memory for hosts (and tests) that do not own a HIP allocator. */
 void* nsh_dev_alloc(size_t bytes);
 int nsh_dev_free(void* p);
+/* The copies wait for the whole device first (every model's stream). */
 int nsh_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int nsh_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int nsh_memset_d(void* dst, int value, size_t bytes);
@@ -81,6 +82,31 @@ int nsh_train_step(ns_model* m, const float* input, const float* labels,
                    size_t input_numel, float* loss_out, float lr);                   /* :2636-2644 */
 int nsh_objective_loss(ns_model* m, const float* input, const float* labels,
                        size_t input_numel, float* loss_out);                         /* :2645-2651 */
+
+/* The other visible symbols of the emitted TU.
+ * nsh_forward: `forward(input, weights, output, n[, moe_active])`
+ * (codegen.cpp:2263-2288): the weights come with the call and are read on
+ * every call; moe_active (MoE plans) NULL = every expert live.  The plan
+ * keeps one model for it (made on the first call, freed with the plan); like
+ * the reference's static buffers it serves one call at a time.
+ * nsh_train_core: `ns_train_core(ctx, x, nx, y, w, wout, loss_out, lr,
+ * train_mode)` (codegen.cpp:2753-3157) over model m: weights read from w,
+ * forward (+ backward and one optimizer step at lr exactly, train_mode != 0),
+ * the loss to *loss_out, the updated weights to wout (train_mode, wout not
+ * NULL); no LR schedule, no step counter (the wrapper's).
+ * nsh_model_set_weights / nsh_model_set_expert_mask: replace the model's
+ * blob (n == weight count) / liveness mask (NULL = all live) and re-sync
+ * the device copies. */
+int nsh_forward(const nsh_plan* p, const float* input, const float* weights, float* output, size_t input_numel,
+                const uint8_t* moe_active);
+int nsh_train_core(ns_model* m, const float* x, size_t nx, const float* y, const float* w, float* wout,
+                   float* loss_out, float lr, int train_mode);
+int nsh_model_set_weights(ns_model* m, const float* w, size_t n);
+int nsh_model_set_expert_mask(ns_model* m, const uint8_t* active);
+/* The wrapper's LR multiplier at step `step` (optim_params.hpp:54-62): the
+ * schedule named by the IR line `// ns.lr_schedule <constant|cosine_warmup>
+ * warmup=W total=T min=F`, constant when absent (the reference's default). */
+float nsh_plan_lr_scale(const nsh_plan* p, int64_t step);
 
 /* Device-resident forward: input/output are device pointers; enqueued on the
  * model's stream, returns before completion (nsh_model_sync waits). */
@@ -220,6 +246,15 @@ int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, i
  * bytes / time. */
 int nsh_bench_mfma_peak(int iters, int blocks, double* tflops);
 int nsh_bench_copy(const float* src, float* dst, int64_t n, int reps, double* gbs);
+/* The row kernels of a training step at one shape (no reference
+ * counterpart), each timed over `reps` back-to-back launches between one
+ * pair of events: us[0..4] = microseconds per launch of the embedding
+ * gather [M] ids of a [V, D] table, LayerNorm and its gradient on [M, D],
+ * the embedding gradient, and softmax cross-entropy with its gradient on
+ * [M, C].  idx: M float ids, labels: [M, C] (device pointers); every other
+ * buffer is allocated and freed by the call. */
+int nsh_bench_rowops(const float* idx, const float* labels, int64_t M, int64_t D, int64_t V, int64_t C, int reps,
+                     double* us);
 
 #ifdef __cplusplus
 }

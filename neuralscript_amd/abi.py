@@ -57,6 +57,7 @@ class NsLib:
             "ns_expert_birth": (sz, [vp, ci]),
             "ns_expert_merge": (sz, [vp, ci, ci]),
             "ns_expert_kill": (sz, [vp, ci]),
+            "ns_train_core": (None, [vp, _f32p, sz, _f32p, _f32p, _f32p, _f32p, cf, ci]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -68,6 +69,13 @@ class NsLib:
                 fn.restype, fn.argtypes = res, args
                 self.has.add(name)
         self.lib = L
+        # the emitted TU's entry function (codegen.cpp:2263-2265); MoE
+        # networks take the liveness mask as a fifth argument
+        self.moe = "ns_expert_count" in self.has
+        self.forward_fn = getattr(L, "forward", None)
+        if self.forward_fn is not None:
+            self.forward_fn.restype = None
+            self.forward_fn.argtypes = [_f32p, _f32p, _f32p, sz] + ([ctypes.c_void_p] if self.moe else [])
 
     def weight_count_static(self):
         return self.lib.ns_weight_count_static()
@@ -127,3 +135,40 @@ class NsLib:
 
     def load(self, m, path):
         return self.lib.ns_load_checkpoint(m, path.encode())
+
+    def forward(self, x, weights, out_numel, moe_active=None):
+        """The entry function `forward(input, weights, output, n[,
+        moe_active])`: weights passed with the call; out_numel floats of
+        output (pre-filled with NaN, so unwritten elements show)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        w = np.ascontiguousarray(weights, dtype=np.float32).ravel()
+        out = np.full(out_numel, np.nan, dtype=np.float32)
+        args = [_fp(x), _fp(w), _fp(out), x.size]
+        if self.moe:
+            mask = None if moe_active is None else np.ascontiguousarray(moe_active, dtype=np.uint8)
+            args.append(None if mask is None else mask.ctypes.data)
+        self.forward_fn(*args)
+        return out
+
+    def train_core(self, ctx, x, labels, weights, lr, train_mode, write_back=True):
+        """`ns_train_core(ctx, x, nx, y, w, wout, loss_out, lr, train_mode)`
+        (codegen.cpp:2753-2755) with w = `weights`: (loss, wout or None)."""
+        x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+        y = np.ascontiguousarray(labels, dtype=np.float32).ravel()
+        w = np.ascontiguousarray(weights, dtype=np.float32).ravel()
+        wout = np.full(w.size, np.nan, dtype=np.float32) if write_back else None
+        loss = np.full(1, np.nan, dtype=np.float32)
+        self.lib.ns_train_core(ctx, _fp(x), x.size, _fp(y), _fp(w), _fp(wout), _fp(loss), ctypes.c_float(lr),
+                               int(train_mode))
+        return loss[0], wout
+
+
+class _RefModel(ctypes.Structure):
+    """The reference CPU driver's model struct (codegen.cpp:2438)."""
+    _fields_ = [("w", ctypes.c_void_p), ("n", ctypes.c_size_t), ("ctx", ctypes.c_void_p)]
+
+
+def reference_ctx(model):
+    """The ns_cpu_ctx of a model made by a reference-emitted CPU driver (its
+    ns_train_core takes the context, not the model)."""
+    return ctypes.cast(ctypes.c_void_p(model), ctypes.POINTER(_RefModel)).contents.ctx

@@ -275,40 +275,32 @@ __global__ __launch_bounds__(kFW * 64) void flash_fwd_kernel(const float* __rest
   }
 }
 
-// Any head size up to 128: one thread per (query, head), two passes over
-// the keys.  Used for small test networks; not a performance path.
-__global__ __launch_bounds__(64) void attention_fwd_small_kernel(const float* __restrict__ Q,
-                                                                 const float* __restrict__ K,
-                                                                 const float* __restrict__ V, float* __restrict__ ctx,
-                                                                 float* __restrict__ lse, int S, int H, int DK,
-                                                                 int64_t ld, float scale) {
-  const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (gid >= (int64_t)S * H) return;
-  const int q = (int)(gid / H), h = (int)(gid % H);
-  const float* qr = Q + (int64_t)q * ld + h * DK;
-  float mx = -INFINITY;
-  for (int j = 0; j < S; j++) {
-    const float* kr = K + (int64_t)j * ld + h * DK;
-    float a = 0.f;
-    for (int d = 0; d < DK; d++) a += qr[d] * kr[d];
-    mx = fmaxf(mx, a * scale);
+// Head sizes the tiled kernels do not take directly (dk not 32, 64 or 128,
+// or rows not 16-byte aligned) run on a padded copy: every head's dk columns
+// padded with zeros to DKP (the next of 32, 64, 128), row pitch H * DKP.
+// Zero columns add nothing to a score q . k and give zero output columns,
+// which unpad drops, so the padded problem computes the same attention (the
+// scale stays 1/sqrt(dk)).
+// dst[s, h*dkp + c] = c < dk ? src[s*ld + h*dk + c] : 0
+__global__ __launch_bounds__(256) void attn_pad_kernel(const float* __restrict__ src, int64_t ld,
+                                                       float* __restrict__ dst, int S, int H, int dk, int dkp) {
+  const int64_t n = (int64_t)S * H * dkp, row = (int64_t)H * dkp;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t s = i / row;
+    const int r = (int)(i - s * row), h = r / dkp, c = r - h * dkp;
+    dst[i] = c < dk ? src[s * ld + (int64_t)h * dk + c] : 0.f;
   }
-  float acc[128];
-  for (int d = 0; d < DK; d++) acc[d] = 0.f;
-  float sum = 0.f;
-  for (int j = 0; j < S; j++) {
-    const float* kr = K + (int64_t)j * ld + h * DK;
-    float a = 0.f;
-    for (int d = 0; d < DK; d++) a += qr[d] * kr[d];
-    const float p = expf(a * scale - mx);
-    sum += p;
-    const float* vr = V + (int64_t)j * ld + h * DK;
-    for (int d = 0; d < DK; d++) acc[d] += p * vr[d];
+}
+
+// dst[s*ld + h*dk + c] = src[s, h*dkp + c] for c < dk
+__global__ __launch_bounds__(256) void attn_unpad_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                         int64_t ld, int S, int H, int dk, int dkp) {
+  const int64_t n = (int64_t)S * H * dk, row = (int64_t)H * dk;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t s = i / row;
+    const int r = (int)(i - s * row), h = r / dk, c = r - h * dk;
+    dst[s * ld + r] = src[s * ((int64_t)H * dkp) + (int64_t)h * dkp + c];
   }
-  float* o = ctx + (int64_t)q * ld + h * DK;
-  for (int d = 0; d < DK; d++) o[d] = acc[d] / sum;
-  // same convention as the flash kernel: log2-sum-exp of scores * scale * log2(e)
-  if (lse) lse[(int64_t)h * S + q] = mx * 1.4426950408889634f + log2f(sum);
 }
 
 
@@ -326,20 +318,6 @@ __global__ __launch_bounds__(64) void attention_fwd_small_kernel(const float* __
 //  * dq: one workgroup per 128 queries loops over key tiles in the forward's
 //    transposed layout (lane = query): dS^T feeds dQ^T = K^T dS^T.
 // ============================================================================
-
-// delta[h*S + q] = sum_{d<DK} dO[q, h*DK + d] * O[q, h*DK + d]
-__global__ __launch_bounds__(256) void attn_delta_kernel(const float* __restrict__ dO, const float* __restrict__ O,
-                                                         float* __restrict__ delta, int S, int H, int DK,
-                                                         int64_t ld) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)S * H) return;
-  const int q = (int)(gid / H), h = (int)(gid % H);
-  const float* a = dO + (int64_t)q * ld + h * DK;
-  const float* b = O + (int64_t)q * ld + h * DK;
-  float acc = 0.f;
-  for (int d = 0; d < DK; d++) acc += a[d] * b[d];
-  delta[(int64_t)h * S + q] = acc;
-}
 
 template <int DK>
 struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
@@ -386,8 +364,10 @@ struct QTile {  // one 64-query tile of Q and dO (row pitch P) plus lse, delta
 
 // STORE_DS: also write dS = P o (dP - delta) (unscaled) to dS[h][query][key]
 // for flash_bwd_dq_ds_kernel; requires S % 64 == 0.
+// Two workgroups per CU up to DK = 64; at DK = 128 a lane's K and V rows and
+// its dK / dV accumulators (4 x DK/2 registers) need one wave per SIMD.
 template <int DK, bool STORE_DS>
-__global__ __launch_bounds__(256, 2) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
+__global__ __launch_bounds__(256, DK >= 128 ? 1 : 2) void flash_bwd_dkdv_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                                                              const float* __restrict__ V, const float* __restrict__ dO,
                                                              const float* __restrict__ lse,
                                                              const float* __restrict__ delta, float* __restrict__ dK,
@@ -740,70 +720,53 @@ __global__ __launch_bounds__(256) void attn_delta_rows_kernel(const float* __res
   }
 }
 
-// Any head size up to 128 (test networks): one thread per (row, head).
-// Pass 1 (per query): dQ.  Pass 2 (per key): dK, dV.
-__global__ __launch_bounds__(64) void attn_bwd_small_q_kernel(const float* __restrict__ Q, const float* __restrict__ K,
-                                                              const float* __restrict__ V,
-                                                              const float* __restrict__ dO,
-                                                              const float* __restrict__ lse,
-                                                              const float* __restrict__ delta, float* __restrict__ dQ,
-                                                              int S, int H, int DK, int64_t ld, float scale,
-                                                              float c_log2) {
-  const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (gid >= (int64_t)S * H) return;
-  const int q = (int)(gid / H), h = (int)(gid % H);
-  const float* qr = Q + (int64_t)q * ld + h * DK;
-  const float* gr = dO + (int64_t)q * ld + h * DK;
-  const float lq = lse[(int64_t)h * S + q], dl = delta[(int64_t)h * S + q];
-  float acc[128];
-  for (int d = 0; d < DK; d++) acc[d] = 0.f;
-  for (int j = 0; j < S; j++) {
-    const float* kr = K + (int64_t)j * ld + h * DK;
-    const float* vr = V + (int64_t)j * ld + h * DK;
-    float s = 0.f, dp = 0.f;
-    for (int d = 0; d < DK; d++) { s += qr[d] * kr[d]; dp += gr[d] * vr[d]; }
-    const float ds = exp2f(s * c_log2 - lq) * (dp - dl);
-    for (int d = 0; d < DK; d++) acc[d] += ds * kr[d];
-  }
-  float* o = dQ + (int64_t)q * ld + h * DK;
-  for (int d = 0; d < DK; d++) o[d] = acc[d] * scale;
-}
-
-__global__ __launch_bounds__(64) void attn_bwd_small_kv_kernel(const float* __restrict__ Q,
-                                                               const float* __restrict__ K,
-                                                               const float* __restrict__ V,
-                                                               const float* __restrict__ dO,
-                                                               const float* __restrict__ lse,
-                                                               const float* __restrict__ delta,
-                                                               float* __restrict__ dK, float* __restrict__ dV, int S,
-                                                               int H, int DK, int64_t ld, float scale,
-                                                               float c_log2) {
-  const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (gid >= (int64_t)S * H) return;
-  const int j = (int)(gid / H), h = (int)(gid % H);
-  const float* kr = K + (int64_t)j * ld + h * DK;
-  const float* vr = V + (int64_t)j * ld + h * DK;
-  float ak[128], av[128];
-  for (int d = 0; d < DK; d++) { ak[d] = 0.f; av[d] = 0.f; }
-  for (int q = 0; q < S; q++) {
-    const float* qr = Q + (int64_t)q * ld + h * DK;
-    const float* gr = dO + (int64_t)q * ld + h * DK;
-    float s = 0.f, dp = 0.f;
-    for (int d = 0; d < DK; d++) { s += qr[d] * kr[d]; dp += gr[d] * vr[d]; }
-    const float p = exp2f(s * c_log2 - lse[(int64_t)h * S + q]);
-    const float ds = p * (dp - delta[(int64_t)h * S + q]);
-    for (int d = 0; d < DK; d++) { av[d] += p * gr[d]; ak[d] += ds * qr[d]; }
-  }
-  for (int d = 0; d < DK; d++) {
-    dK[(int64_t)j * ld + h * DK + d] = ak[d] * scale;
-    dV[(int64_t)j * ld + h * DK + d] = av[d];
-  }
-}
-
 }  // namespace
 
+// The tiled kernels' head sizes; others are padded to the next one.
+static int64_t padded_dk(int64_t dk) { return dk <= 32 ? 32 : dk <= 64 ? 64 : dk <= 128 ? 128 : 0; }
+
+bool attention_in_place(int64_t D, int64_t H, int64_t ld, const void* const* ptrs, int n) {
+  if (H <= 0 || D % H != 0 || ld % 4 != 0) return false;
+  const int64_t dk = D / H;
+  if (dk != 32 && dk != 64 && dk != 128) return false;
+  for (int i = 0; i < n; i++)
+    if ((uintptr_t)ptrs[i] % 16 != 0) return false;
+  return true;
+}
+
+size_t attention_pad_floats(int64_t S, int64_t D, int64_t H, bool backward) {
+  if (S <= 0 || H <= 0 || D % H != 0) return 0;
+  const int64_t dkp = padded_dk(D / H);
+  // forward: Q K V ctx; backward: Q K V O dO dQ dK dV
+  return (size_t)((backward ? 8 : 4) * S * H * dkp);
+}
+
+static int pad_copy(const float* src, int64_t ld, float* dst, int64_t S, int64_t H, int64_t dk, int64_t dkp,
+                    hipStream_t s) {
+  const unsigned g = (unsigned)std::min<int64_t>(ceil_div(S * H * dkp, 256), 16384);
+  hipLaunchKernelGGL(attn_pad_kernel, dim3(g), dim3(256), 0, s, src, ld, dst, (int)S, (int)H, (int)dk, (int)dkp);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+static int unpad_copy(const float* src, float* dst, int64_t ld, int64_t S, int64_t H, int64_t dk, int64_t dkp,
+                      hipStream_t s) {
+  const unsigned g = (unsigned)std::min<int64_t>(ceil_div(S * H * dk, 256), 16384);
+  hipLaunchKernelGGL(attn_unpad_kernel, dim3(g), dim3(256), 0, s, src, dst, ld, (int)S, (int)H, (int)dk, (int)dkp);
+  NSH_LAUNCHED();
+  return 0;
+}
+
+template <int DK>
+static void flash_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t H,
+                      int64_t ld, float scale, hipStream_t s) {
+  const int nqb = (int)ceil_div(S, 32 * kFW);
+  hipLaunchKernelGGL(flash_fwd_kernel<DK>, dim3(nqb * (unsigned)H), dim3(64 * kFW), 0, s, Q, K, V, ctx, lse, (int)S,
+                     (int)H, ld, scale * 1.4426950408889634f, nqb);
+}
+
 int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, hipStream_t s) {
+                         int64_t H, int64_t ld, float* pad_ws, hipStream_t s) {
   if (S <= 0) return 0;
   if (H <= 0 || D % H != 0 || S > INT32_MAX) {
     set_error("attention: bad shape");
@@ -811,94 +774,106 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
   }
   const int64_t DK = D / H;
   const float scale = 1.0f / sqrtf((float)DK);
-  const bool aligned = ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V) % 16 == 0;
-  if (aligned && (DK == 64 || DK == 32)) {
-    const int nqb = (int)ceil_div(S, 32 * kFW);
-    const dim3 grid(nqb * (unsigned)H), block(64 * kFW);
-    const float sl2 = scale * 1.4426950408889634f;
-    if (DK == 64)
-      hipLaunchKernelGGL(flash_fwd_kernel<64>, grid, block, 0, s, Q, K, V, ctx, lse, (int)S, (int)H, ld, sl2, nqb);
-    else
-      hipLaunchKernelGGL(flash_fwd_kernel<32>, grid, block, 0, s, Q, K, V, ctx, lse, (int)S, (int)H, ld, sl2, nqb);
-  } else {
-    if (DK > 128) {
-      set_error("attention: head size above 128 is not supported");
-      return -1;
-    }
-    hipLaunchKernelGGL(attention_fwd_small_kernel, dim3((unsigned)ceil_div(S * H, 64)), dim3(64), 0, s, Q, K, V, ctx,
-                       lse, (int)S, (int)H, (int)DK, ld, scale);
+  const void* ptrs[3] = {Q, K, V};  // read as float4 rows
+  if (attention_in_place(D, H, ld, ptrs, 3)) {
+    if (DK == 128) flash_fwd<128>(Q, K, V, ctx, lse, S, H, ld, scale, s);
+    else if (DK == 64) flash_fwd<64>(Q, K, V, ctx, lse, S, H, ld, scale, s);
+    else flash_fwd<32>(Q, K, V, ctx, lse, S, H, ld, scale, s);
+    NSH_LAUNCHED();
+    return 0;
   }
+  const int64_t dkp = padded_dk(DK);
+  if (!dkp) {
+    set_error("attention: head size above 128 is not supported");
+    return -1;
+  }
+  if (!pad_ws) {
+    set_error("attention: this head size or alignment needs the padding workspace");
+    return -1;
+  }
+  const int64_t ldp = H * dkp, n = S * ldp;
+  float *Qp = pad_ws, *Kp = pad_ws + n, *Vp = pad_ws + 2 * n, *Op = pad_ws + 3 * n;
+  if (pad_copy(Q, ld, Qp, S, H, DK, dkp, s) || pad_copy(K, ld, Kp, S, H, DK, dkp, s) ||
+      pad_copy(V, ld, Vp, S, H, DK, dkp, s))
+    return -1;
+  if (dkp == 128) flash_fwd<128>(Qp, Kp, Vp, Op, lse, S, H, ldp, scale, s);
+  else if (dkp == 64) flash_fwd<64>(Qp, Kp, Vp, Op, lse, S, H, ldp, scale, s);
+  else flash_fwd<32>(Qp, Kp, Vp, Op, lse, S, H, ldp, scale, s);
   NSH_LAUNCHED();
-  return 0;
+  return unpad_copy(Op, ctx, ld, S, H, DK, dkp, s);
 }
 
 size_t attention_bwd_ds_floats(int64_t S, int64_t D, int64_t H) {
-  if (S <= 0 || H <= 0 || D % H != 0 || S % kBK != 0) return 0;
-  const int64_t DK = D / H;
-  if (DK != 32 && DK != 64) return 0;
+  if (S <= 0 || H <= 0 || D % H != 0 || S % kBK != 0 || !padded_dk(D / H)) return 0;
   const double bytes = 4.0 * (double)H * (double)S * (double)S;
   if (bytes > 16.0 * 1024 * 1024 * 1024) return 0;  // recompute beyond 16 GiB
   return (size_t)(H * S * S);
 }
 
+// The backward kernels of one tile width on arrays of row pitch ld.
+template <int DK>
+static int flash_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
+                     const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t H,
+                     int64_t ld, float scale, float* ds_ws, hipStream_t s) {
+  const float cl2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_delta_rows_kernel<DK>, dim3((unsigned)ceil_div(S, 4)), dim3(256), 0, s, dO, O, delta,
+                     (int)S, (int)H, ld);
+  NSH_LAUNCHED();
+  const int nb = (int)ceil_div(S, kBQ);
+  const dim3 grid(nb * (unsigned)H), block(256);
+  if (ds_ws) {
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK, true>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, ds_ws,
+                       (int)S, (int)H, ld, scale, cl2, nb);
+    hipLaunchKernelGGL(flash_bwd_dq_ds_kernel<DK>, grid, block, 0, s, K, ds_ws, dQ, (int)S, (int)H, ld, scale, nb);
+  } else {
+    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK, false>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV,
+                       nullptr, (int)S, (int)H, ld, scale, cl2, nb);
+    hipLaunchKernelGGL(flash_bwd_dq_kernel<DK>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,
+                       scale, cl2, nb);
+  }
+  NSH_LAUNCHED();
+  return 0;
+}
+
+template <typename... A>
+static int flash_bwd_any(int64_t dk, A... a) {
+  return dk == 128 ? flash_bwd<128>(a...) : dk == 64 ? flash_bwd<64>(a...) : flash_bwd<32>(a...);
+}
+
 int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                          const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, float* ds_ws, hipStream_t s) {
+                         int64_t H, int64_t ld, float* ds_ws, float* pad_ws, hipStream_t s) {
   if (S <= 0) return 0;
   if (H <= 0 || D % H != 0 || S > INT32_MAX) {
     set_error("attention backward: bad shape");
     return -1;
   }
   const int64_t DK = D / H;
-  if (DK > 128) {
+  const float scale = 1.0f / sqrtf((float)DK);
+  float* ds = ds_ws && attention_bwd_ds_floats(S, D, H) > 0 && ((uintptr_t)ds_ws % 16) == 0 ? ds_ws : nullptr;
+  const void* ptrs[5] = {Q, K, V, O, dO};  // read as float4 rows
+  if (attention_in_place(D, H, ld, ptrs, 5))
+    return flash_bwd_any(DK, Q, K, V, O, dO, lse, delta, dQ, dK, dV, S, H, ld, scale, ds, s);
+  const int64_t dkp = padded_dk(DK);
+  if (!dkp) {
     set_error("attention: head size above 128 is not supported");
     return -1;
   }
-  const float scale = 1.0f / sqrtf((float)DK);
-  const float cl2 = scale * 1.4426950408889634f;
-  const bool aligned =
-      ld % 4 == 0 && ((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)dO | (uintptr_t)O) % 16 == 0;
-  const bool flash = aligned && (DK == 64 || DK == 32);
-  if (flash) {
-    const dim3 g((unsigned)ceil_div(S, 4));
-    if (DK == 64)
-      hipLaunchKernelGGL(attn_delta_rows_kernel<64>, g, dim3(256), 0, s, dO, O, delta, (int)S, (int)H, ld);
-    else
-      hipLaunchKernelGGL(attn_delta_rows_kernel<32>, g, dim3(256), 0, s, dO, O, delta, (int)S, (int)H, ld);
-  } else {
-    hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)ceil_div(S * H, 256)), dim3(256), 0, s, dO, O, delta, (int)S,
-                       (int)H, (int)DK, ld);
+  if (!pad_ws) {
+    set_error("attention backward: this head size or alignment needs the padding workspace");
+    return -1;
   }
-  NSH_LAUNCHED();
-  if (flash) {
-    const int nb = (int)ceil_div(S, kBQ);
-    const dim3 grid(nb * (unsigned)H), block(256);
-    const bool use_ds = ds_ws && attention_bwd_ds_floats(S, D, H) > 0 && ((uintptr_t)ds_ws % 16) == 0;
-#define NSH_BWD(DK_)                                                                                                  \
-  if (use_ds) {                                                                                                       \
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK_, true>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV, ds_ws, \
-                       (int)S, (int)H, ld, scale, cl2, nb);                                                           \
-    hipLaunchKernelGGL(flash_bwd_dq_ds_kernel<DK_>, grid, block, 0, s, K, ds_ws, dQ, (int)S, (int)H, ld, scale, nb); \
-  } else {                                                                                                            \
-    hipLaunchKernelGGL((flash_bwd_dkdv_kernel<DK_, false>), grid, block, 0, s, Q, K, V, dO, lse, delta, dK, dV,      \
-                       nullptr, (int)S, (int)H, ld, scale, cl2, nb);                                                  \
-    hipLaunchKernelGGL(flash_bwd_dq_kernel<DK_>, grid, block, 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H, ld,  \
-                       scale, cl2, nb);                                                                               \
-  }
-    if (DK == 64) {
-      NSH_BWD(64)
-    } else {
-      NSH_BWD(32)
-    }
-#undef NSH_BWD
-  } else {
-    const dim3 grid((unsigned)ceil_div(S * H, 64));
-    hipLaunchKernelGGL(attn_bwd_small_q_kernel, grid, dim3(64), 0, s, Q, K, V, dO, lse, delta, dQ, (int)S, (int)H,
-                       (int)DK, ld, scale, cl2);
-    hipLaunchKernelGGL(attn_bwd_small_kv_kernel, grid, dim3(64), 0, s, Q, K, V, dO, lse, delta, dK, dV, (int)S, (int)H,
-                       (int)DK, ld, scale, cl2);
-  }
-  NSH_LAUNCHED();
+  const int64_t ldp = H * dkp, n = S * ldp;
+  float* p[8];
+  for (int i = 0; i < 8; i++) p[i] = pad_ws + i * n;
+  const float* src[5] = {Q, K, V, O, dO};
+  for (int i = 0; i < 5; i++)
+    if (pad_copy(src[i], ld, p[i], S, H, DK, dkp, s) != 0) return -1;
+  if (flash_bwd_any(dkp, p[0], p[1], p[2], p[3], p[4], lse, delta, p[5], p[6], p[7], S, H, ldp, scale, ds, s) != 0)
+    return -1;
+  float* dst[3] = {dQ, dK, dV};
+  for (int i = 0; i < 3; i++)
+    if (unpad_copy(p[5 + i], dst[i], ld, S, H, DK, dkp, s) != 0) return -1;
   return 0;
 }
 

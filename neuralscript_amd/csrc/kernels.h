@@ -78,8 +78,15 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
 // ctx[S, D] (heads concatenated) = softmax(Q_h K_h^T * scale) V_h per head,
 // Q/K/V row-major [S, D] with row pitch ld.  lse (optional, [H, S]) receives
 // log2(sum_j 2^(s_j * scale * log2 e)) per query, for the backward pass.
+// Head sizes 32, 64 and 128 on 16-byte aligned rows (ld % 4 == 0) run in
+// place (attention_in_place over the arrays read as float4 rows: Q, K, V,
+// and O, dO in the backward); every other head size up to 128 runs on a copy
+// padded with zero columns to the next of them, in pad_ws
+// (attention_pad_floats floats); above 128 is refused.
+bool attention_in_place(int64_t D, int64_t H, int64_t ld, const void* const* ptrs, int n);
+size_t attention_pad_floats(int64_t S, int64_t D, int64_t H, bool backward);
 int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, hipStream_t s);
+                         int64_t H, int64_t ld, float* pad_ws, hipStream_t s);
 
 // Backward of the core: dQ, dK, dV [S, D] (row pitch ld) from dO = d ctx, the
 // forward's ctx (O) and lse; delta: [H, S] workspace.  ds_ws (optional, 16-byte
@@ -89,7 +96,7 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
 size_t attention_bwd_ds_floats(int64_t S, int64_t D, int64_t H);
 int launch_attention_bwd(const float* Q, const float* K, const float* V, const float* O, const float* dO,
                          const float* lse, float* delta, float* dQ, float* dK, float* dV, int64_t S, int64_t D,
-                         int64_t H, int64_t ld, float* ds_ws, hipStream_t s);
+                         int64_t H, int64_t ld, float* ds_ws, float* pad_ws, hipStream_t s);
 
 // optim.hip --------------------------------------------------------------------
 int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1t, float b2t,
@@ -118,6 +125,8 @@ int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
 // buffer of 256 floats.
 int bench_mfma_peak(int iters, int blocks, float* out, float* ms);
 int bench_copy(const float* src, float* dst, int64_t n, int reps, float* ms);
+int bench_rowops(const float* idx, const float* labels, int64_t M, int64_t D, int64_t V, int64_t C, int reps,
+                 double* us);
 
 // movement.hip -------------------------------------------------------------------
 int launch_binop(const float* A, const float* B, float* C, int64_t na, int64_t nb, int code, hipStream_t s);

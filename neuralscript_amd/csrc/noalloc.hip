@@ -63,10 +63,11 @@ using namespace nship;
 
 extern "C" int nsh_op_embedding_grad_noalloc(const float* dout, const float* idx, float* dW, int64_t n, int64_t V,
                                              int64_t D, void* stream) {
-  if (!dW || n < 0 || V <= 0 || D <= 0 || (n > 0 && (!dout || !idx))) {
+  if (n < 0 || V < 0 || D < 0 || (V * D > 0 && !dW) || (n > 0 && (!dout || !idx))) {
     set_error("embedding_grad_noalloc: null pointer or bad size");
     return -1;
   }
+  if (V == 0 || D == 0) return 0;  // dW is empty, as in nsh_op_embedding_grad
   if ((int64_t)embedding_grad_workspace(n, V) > kScratchInts) {
     set_error("embedding_grad_noalloc: 3*V + 1 + 2*n = " + std::to_string(embedding_grad_workspace(n, V)) +
               " ints exceeds the static scratch of " + std::to_string(kScratchInts) +

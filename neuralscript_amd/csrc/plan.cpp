@@ -9,6 +9,7 @@
 #include "plan.h"
 
 #include <cctype>
+#include <cmath>
 #include <cstdlib>
 #include <sstream>
 
@@ -119,7 +120,38 @@ bool parse_line(const std::string& line, Raw* r, std::string* err) {
   return true;
 }
 
+// `// ns.lr_schedule <kind> warmup=W total=T min=F`; false on a malformed line.
+bool parse_lr_schedule(const std::string& line, LrSchedule* s) {
+  std::istringstream is(line.substr(line.find("ns.lr_schedule") + 14));
+  std::string kind, tok;
+  is >> kind;
+  if (kind == "constant") s->kind = 0;
+  else if (kind == "cosine_warmup") s->kind = 1;
+  else return false;
+  while (is >> tok) {
+    const size_t eq = tok.find('=');
+    if (eq == std::string::npos) return false;
+    const std::string k = tok.substr(0, eq), v = tok.substr(eq + 1);
+    char* e = nullptr;
+    if (k == "warmup") s->warmup = std::strtoll(v.c_str(), &e, 10);
+    else if (k == "total") s->total = std::strtoll(v.c_str(), &e, 10);
+    else if (k == "min") s->min_factor = std::strtof(v.c_str(), &e);
+    else return false;
+    if (v.empty() || *e != '\0') return false;
+  }
+  return true;
+}
+
 }  // namespace
+
+float lr_scale(const LrSchedule& s, int64_t step) {
+  if (s.kind == 0) return 1.0f;
+  if (step < s.warmup) return s.warmup > 0 ? (float)step / (float)s.warmup : 1.0f;
+  const int64_t end = s.total > s.warmup ? s.total : s.warmup + 1;
+  const int64_t st = step >= end ? end : step;
+  const float t = (float)(st - s.warmup) / (float)(end - s.warmup);
+  return s.min_factor + 0.5f * (1.0f - s.min_factor) * (1.0f + cosf(3.14159265f * t));
+}
 
 Plan* parse_plan(const char* text, std::string* err) {
   if (!text) {
@@ -153,6 +185,10 @@ Plan* parse_plan(const char* text, std::string* err) {
   std::string line;
   while (std::getline(in, line)) {
     line = trim(line);
+    if (starts(line, "// ns.lr_schedule")) {
+      if (!parse_lr_schedule(line, &P->lr)) return fail("bad lr schedule line: " + line);
+      continue;
+    }
     if (line.empty() || starts(line, "//")) continue;
     if (starts(line, "ns.func @")) {
       funcs.push_back(RawFunc());

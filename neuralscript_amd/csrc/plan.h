@@ -75,7 +75,20 @@ struct MoeInfo {
   int g = -1, e1 = -1, e2 = -1;  // weight value ids
 };
 
+// The runtime wrapper's learning-rate multiplier (optim_params.hpp:36-62),
+// compiled into the reference's driver from optim::kLRSchedule and carried
+// here by the IR line `// ns.lr_schedule <kind> warmup=W total=T min=F`
+// (kind constant | cosine_warmup; absent: constant, the reference default).
+struct LrSchedule {
+  int kind = 0;  // 0 constant, 1 linear warmup then cosine decay
+  int64_t warmup = 100, total = 10000;
+  float min_factor = 0.05f;
+};
+// Multiplier at wrapper step `step` (codegen.cpp:23-39 / optim_params.hpp:54-62).
+float lr_scale(const LrSchedule& s, int64_t step);
+
 struct Plan {
+  LrSchedule lr;
   std::vector<Value> vals;
   std::map<std::string, int> index;
   std::vector<int> weights;  // value ids in TENSOR_ALLOC order

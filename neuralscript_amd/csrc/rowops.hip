@@ -10,9 +10,10 @@
 // One wave owns one row: the row is loaded once into registers (float4,
 // coalesced), reduced with xor-shuffles, and written once, so each kernel
 // moves the algorithmic minimum of bytes.  The embedding gradient is
-// deterministic and bit-exact: tokens are grouped by row with a stable
-// counting sort and each output element sums its tokens in token order, as
-// the reference's sequential scatter-add does.
+// deterministic and bit-exact: each output element sums its tokens in token
+// order, as the reference's sequential scatter-add does -- in one launch
+// through per-row token bitmaps in LDS up to 32768 tokens, beyond that
+// through a stable counting sort of the tokens by row.
 #include <algorithm>
 
 #include "common.h"
@@ -610,6 +611,128 @@ __global__ __launch_bounds__(256) void emb_grad_rows_vec_kernel(const float* __r
   }
 }
 
+// ---- embedding weight gradient in one launch (no sort, no workspace) --------
+// Each workgroup owns kEmbRowsPerWg consecutive vocabulary rows.  It reads
+// every token id once (the ids are shared by all workgroups, so they come
+// from L2) and marks the tokens that hit its rows in one LDS bitmap per row,
+// bit t = token t.  Walking a row's bitmap word by word and bit by bit
+// visits its tokens in ascending order, so each output element is the
+// reference's sequential sum with no sort at all.  One wave per row: it
+// gathers the row's tokens' gradient rows (kEmbAhead loads in flight) and
+// adds them in token order, then writes the dW row once (zeros if no token).
+constexpr int kEmbRowsPerWg = 16;  // 16 waves of 64 lanes
+// LDS budget of the bitmaps: kEmbRowsPerWg * ceil(n/32) words.
+constexpr int64_t kEmbFusedMaxTokens = 32768;
+
+template <bool VEC, int NV, int kEmbAhead>
+__global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __restrict__ dout,
+                                                              const float* __restrict__ idx,
+                                                              float* __restrict__ dW, int64_t n, int64_t V,
+                                                              int64_t D) {
+  extern __shared__ unsigned emb_bits[];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int nw = (int)((n + 31) >> 5);
+  const int64_t r0 = (int64_t)blockIdx.x * kEmbRowsPerWg;
+  for (int i = t; i < kEmbRowsPerWg * nw; i += 1024) emb_bits[i] = 0u;
+  __syncthreads();
+  // ids in batches of 8 per thread, all 8 loads issued before any is used
+  for (int64_t base = 0; base < n; base += 8 * 1024) {
+    float f[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int64_t i = base + k * 1024 + t;
+      f[k] = i < n ? idx[i] : -1.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int64_t i = base + k * 1024 + t;
+      const int64_t lr = emb_row(f[k], V) - r0;  // out of range (and i >= n): -1 - r0 < 0
+      if (lr >= 0 && lr < kEmbRowsPerWg)
+        atomicOr(&emb_bits[(int)lr * nw + (int)(i >> 5)], 1u << (i & 31));
+    }
+  }
+  __syncthreads();
+  const int64_t r = r0 + wv;
+  if (r >= V) return;
+  const unsigned* __restrict__ bits = emb_bits + wv * nw;
+  // Columns per pass: 64 lanes x NV float4 (VEC) or 64 lanes x NV floats.
+  constexpr int W = VEC ? 4 : 1;
+  const int64_t DW = D / W;
+  // The pass loop is wave-uniform (every lane takes part in the ballots and
+  // lane reads below); lanes past the row's end only skip their loads/stores.
+  for (int64_t cb = 0; cb < DW; cb += 64 * NV) {
+    const int64_t c0 = cb + lane;
+    float acc[NV][W];
+    float buf[kEmbAhead][NV][W];
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+#pragma unroll
+      for (int k = 0; k < W; k++) acc[j][k] = 0.f;
+    int pend = 0;  // loads in flight, oldest in slot (head % kEmbAhead)
+    int head = 0;
+    auto add_oldest = [&]() {
+      const int s = head % kEmbAhead;
+#pragma unroll
+      for (int q = 0; q < kEmbAhead; q++)
+        if (q == s)
+#pragma unroll
+          for (int j = 0; j < NV; j++)
+#pragma unroll
+            for (int k = 0; k < W; k++) acc[j][k] += buf[q][j][k];
+      head++;
+      pend--;
+    };
+    for (int w0 = 0; w0 < nw; w0 += 64) {
+      const unsigned word = w0 + lane < nw ? bits[w0 + lane] : 0u;
+      uint64_t nz = __ballot(word != 0u);
+      while (nz) {
+        const int l = __builtin_ctzll(nz);
+        nz &= nz - 1;
+        unsigned wd = (unsigned)__builtin_amdgcn_readlane((int)word, l);
+        while (wd) {
+          const int b = __builtin_ctz(wd);
+          wd &= wd - 1;
+          const int64_t tok = (int64_t)(w0 + l) * 32 + b;
+          if (pend == kEmbAhead) add_oldest();
+          const int s = (head + pend) % kEmbAhead;
+          const float* src = dout + tok * D;
+#pragma unroll
+          for (int q = 0; q < kEmbAhead; q++)
+            if (q == s)
+#pragma unroll
+              for (int j = 0; j < NV; j++) {
+                const int64_t c = c0 + 64 * j;
+                if (c < DW) {
+                  if constexpr (VEC) {
+                    const float4 v = reinterpret_cast<const float4*>(src)[c];
+                    buf[q][j][0] = v.x; buf[q][j][1] = v.y; buf[q][j][2] = v.z; buf[q][j][3] = v.w;
+                  } else {
+                    buf[q][j][0] = src[c];
+                  }
+                } else {
+#pragma unroll
+                  for (int k = 0; k < W; k++) buf[q][j][k] = 0.f;
+                }
+              }
+          pend++;
+        }
+      }
+    }
+    while (pend > 0) add_oldest();
+    float* o = dW + r * D;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+      const int64_t c = c0 + 64 * j;
+      if (c < DW) {
+        if constexpr (VEC)
+          reinterpret_cast<float4*>(o)[c] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+        else
+          o[c] = acc[j][0];
+      }
+    }
+  }
+}
+
 // Clears n ints.  A kernel rather than hipMemsetAsync, so that a caller may
 // capture the launch sequence in a HIP graph (memset nodes are avoided).
 __global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p, int64_t n) {
@@ -619,8 +742,38 @@ __global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p
 // Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
 size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
 
+// One launch without workspace when the bitmaps fit in 64 KB of LDS and
+// the workgroups' shared reads of the ids stay small (n ids per workgroup).
+static bool emb_grad_fused_fits(int64_t n, int64_t V) {
+  return n <= kEmbFusedMaxTokens && n * ceil_div(V, kEmbRowsPerWg) <= ((int64_t)1 << 26);
+}
+
+template <bool VEC>
+static void launch_emb_grad_fused(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                                  hipStream_t s) {
+  const dim3 g((unsigned)ceil_div(V, kEmbRowsPerWg));
+  const size_t lds = (size_t)kEmbRowsPerWg * (size_t)((n + 31) >> 5) * sizeof(unsigned);
+  const int64_t DW = VEC ? D / 4 : D;
+  // NV columns per lane per pass, AH rows in flight: NV * AH float4 of loads
+  if (DW > 128)
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+  else if (DW > 64)
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+  else
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+}
+
 int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D, int* ws,
                           hipStream_t s) {
+  if (V <= 0 || D <= 0) return 0;  // dW is empty
+  if (emb_grad_fused_fits(n, V)) {
+    if (D % 4 == 0 && ((uintptr_t)dout | (uintptr_t)dW) % 16 == 0)
+      launch_emb_grad_fused<true>(dout, idx, dW, n, V, D, s);
+    else
+      launch_emb_grad_fused<false>(dout, idx, dW, n, V, D, s);
+    NSH_LAUNCHED();
+    return 0;
+  }
   int* count = ws;
   int* start = ws + V;
   int* cursor = ws + 2 * V + 1;
@@ -628,7 +781,7 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
   int* tmp = order + n;
   // count [0, V) and cursor [2V+1, 3V+1) start at zero; start in between is
   // written whole by the scan, so one fill covers [0, 3V+1)
-  if (V > 0) {
+  {
     const int64_t nz = 3 * V + 1;
     hipLaunchKernelGGL(fill_zero_ints_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(nz, 256), 1024)), dim3(256), 0,
                        s, ws, nz);

@@ -50,6 +50,7 @@ using namespace nship;
 
 struct nsh_plan {
   std::unique_ptr<Plan> p;
+  ns_model* fwd = nullptr;  // the model behind nsh_forward, made on its first call
 };
 
 struct ns_model {
@@ -59,6 +60,7 @@ struct ns_model {
   std::vector<float> h_w;
   bool host_stale = false;  // device blob newer than h_w
   bool device_stale = false;  // h_w newer than the device blob (a failed upload)
+  bool mask_stale = false;    // moe_active newer than d_active (a failed mask upload)
   std::vector<uint8_t> moe_active;
   size_t moe_count = 0;
   uint8_t* d_active = nullptr;
@@ -358,8 +360,12 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
       }
       {
         Prof p(m, "attention_fwd");
+        const void* qkv[3] = {sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D};
+        float* pad = nullptr;
+        if (!attention_in_place(D, H, D, qkv, 3) && !(pad = scratch(m, "attn_pad", attention_pad_floats(BS, D, H, false))))
+          return -1;
         if (launch_attention_fwd(sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, train ? sv.lse : nullptr, BS, D,
-                                 H, D, s) != 0)
+                                 H, D, pad, s) != 0)
           return -1;
       }
       Prof p(m, "gemm");
@@ -621,8 +627,12 @@ int attention_backward(ns_model* m, Frame& fr, const Instr& I, AttnGrads* out) {
     const size_t nds = attention_bwd_ds_floats(BS, D, H);
     float* ds = nds ? scratch(m, "attn_ds", nds) : nullptr;
     if (nds && !ds) return -1;
+    const void* rd[5] = {sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, dPre};
+    float* pad = nullptr;
+    if (!attention_in_place(D, H, D, rd, 5) && !(pad = scratch(m, "attn_pad", attention_pad_floats(BS, D, H, true))))
+      return -1;
     if (launch_attention_bwd(sv.qkv, sv.qkv + BS * D, sv.qkv + 2 * BS * D, sv.ctx, dPre, sv.lse, delta, dqkv,
-                             dqkv + BS * D, dqkv + 2 * BS * D, BS, D, H, D, ds, s) != 0)
+                             dqkv + BS * D, dqkv + 2 * BS * D, BS, D, H, D, ds, pad, s) != 0)
       return -1;
   }
   Prof p(m, "gemm");
@@ -1049,10 +1059,11 @@ int upload_mask(ns_model* m) {
                                 m->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   if (e != hipSuccess) {
-    m->device_stale = true;
+    m->mask_stale = true;  // only the mask: the device weights may be newer than h_w
     set_error(std::string("mask upload: ") + hipGetErrorString(e));
     return -1;
   }
+  m->mask_stale = false;
   return 0;
 }
 
@@ -1062,9 +1073,11 @@ int device_sync_weights(ns_model* m) {
   return 0;
 }
 
-// Before any device work: a lifecycle edit whose upload failed is re-sent.
+// Before any device work: a lifecycle edit whose upload failed is re-sent
+// (the whole blob after a failed weight upload, else only a failed mask).
 int ensure_device_current(ns_model* m) {
-  return m->device_stale ? device_sync_weights(m) : 0;
+  if (m->device_stale) return device_sync_weights(m);
+  return m->mask_stale ? upload_mask(m) : 0;
 }
 
 }  // namespace
@@ -1098,12 +1111,18 @@ int nsh_dev_free(void* p) {
   return 0;
 }
 
+// The copies first wait for the whole device: a model's work runs on its own
+// non-blocking stream, which a null-stream hipMemcpy would not wait for, so
+// a read right after nsh_eval_infer_device / nsh_train_step_device sees the
+// finished results (and a write cannot overtake kernels still reading).
 int nsh_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  NSH_CHECK(hipDeviceSynchronize());
   NSH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
   return 0;
 }
 
 int nsh_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  NSH_CHECK(hipDeviceSynchronize());
   NSH_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
   return 0;
 }
@@ -1131,7 +1150,10 @@ nsh_plan* nsh_plan_parse(const char* ir_text) {
   return h;
 }
 
-void nsh_plan_free(nsh_plan* p) { delete p; }
+void nsh_plan_free(nsh_plan* p) {
+  if (p && p->fwd) nsh_model_free(p->fwd);
+  delete p;
+}
 size_t nsh_plan_weight_count(const nsh_plan* p) { return p ? p->p->total : 0; }
 const ns_weight_layout* nsh_plan_layout(const nsh_plan* p) { return p ? &p->p->layout : nullptr; }
 size_t nsh_plan_output_numel(const nsh_plan* p, size_t input_numel) {
@@ -1340,7 +1362,8 @@ size_t nsh_expert_birth(ns_model* m, int n) {
     n--;
     if (upload_weights(m, o1 + g2, D * H) != 0 || upload_weights(m, o2 + g3, H * D) != 0) return m->moe_count;
   }
-  // (a failed upload leaves device_stale set: the next device call retries)
+  // (a failed upload leaves device_stale or mask_stale set: the next device
+  // call retries)
   if (upload_weights(m, og, D * cap) == 0) upload_mask(m);
   return m->moe_count;
 }
@@ -1381,8 +1404,9 @@ size_t nsh_expert_kill(ns_model* m, int k) {
   return m->moe_count;
 }
 
-// Host-pointer training step: the wrapper of codegen.cpp:2636-2644 (LR
-// schedule step counter; the compiled-in schedule is constant, multiplier 1).
+// Training step: the wrapper of codegen.cpp:2636-2644 -- the plan's LR
+// schedule multiplier at the model's step counter (post-incremented,
+// saturating); the reference compiles the constant schedule (multiplier 1).
 int nsh_train_step_device(ns_model* m, const float* d_input, const float* d_labels, size_t input_numel,
                           float* loss_out, float lr) {
   if (!m || !d_input || !d_labels) {
@@ -1395,7 +1419,7 @@ int nsh_train_step_device(ns_model* m, const float* d_input, const float* d_labe
   }
   const int64_t st = m->lr_step;
   if (st < INT64_MAX) m->lr_step = st + 1;
-  const float lr_eff = lr * 1.0f;
+  const float lr_eff = lr * lr_scale(m->plan->lr, st);
   float* d_loss = nullptr;
   if (run_train(m, d_input, input_numel, d_labels, lr_eff, true, &d_loss) != 0) return -1;
   if (loss_out) {
@@ -1461,6 +1485,87 @@ int nsh_objective_loss(ns_model* m, const float* input, const float* labels, siz
   NSH_CHECK(hipMemcpyAsync(&loss, d_loss, sizeof(float), hipMemcpyDeviceToHost, m->stream));
   if (sync(m) != 0) return -1;
   if (loss_out) *loss_out = loss;
+  return 0;
+}
+
+float nsh_plan_lr_scale(const nsh_plan* p, int64_t step) { return p ? lr_scale(p->p->lr, step) : 1.0f; }
+
+// ---- stateless entry points of the emitted TU --------------------------------
+int nsh_model_set_weights(ns_model* m, const float* w, size_t n) {
+  if (!m || !w || n != m->plan->total) {
+    set_error("set_weights: null argument or weight count mismatch");
+    return -1;
+  }
+  if (sync(m) != 0) return -1;  // kernels of an earlier device-pointer call read the blob
+  std::memcpy(m->h_w.data(), w, n * sizeof(float));
+  m->host_stale = false;
+  return device_sync_weights(m);
+}
+
+int nsh_model_set_expert_mask(ns_model* m, const uint8_t* active) {
+  if (!m) return -1;
+  const MoeInfo& q = m->plan->moe;
+  if (!q.present) return 0;
+  if (sync(m) != 0) return -1;
+  size_t live = 0;
+  for (int64_t e = 0; e < q.E; e++) {
+    m->moe_active[(size_t)e] = (!active || active[e] != 0) ? 1 : 0;
+    live += m->moe_active[(size_t)e];
+  }
+  m->moe_count = live;
+  return upload_mask(m);
+}
+
+// The emitted TU's `forward` (codegen.cpp:2263-2288): the weights come with
+// every call, and every call reads them (the reference re-assigns its
+// per-weight buffers from `weights`); moe_active NULL = every expert live
+// (ns_moe_fwd's `active == NULL`).  One cached model per plan holds the
+// device state; like the reference's static buffers it serves one call at a
+// time.
+int nsh_forward(const nsh_plan* p, const float* input, const float* weights, float* output, size_t input_numel,
+                const uint8_t* moe_active) {
+  if (!p || !input || !weights || !output) {
+    set_error("forward: null argument");
+    return -1;
+  }
+  nsh_plan* ph = const_cast<nsh_plan*>(p);
+  if (!ph->fwd) {
+    ph->fwd = nsh_model_init(p, weights, p->p->total);
+    if (!ph->fwd) return -1;
+  } else if (nsh_model_set_weights(ph->fwd, weights, p->p->total) != 0) {
+    return -1;
+  }
+  if (nsh_model_set_expert_mask(ph->fwd, moe_active) != 0) return -1;
+  return nsh_eval_infer(ph->fwd, input, output, input_numel);
+}
+
+// The emitted TU's `ns_train_core` (codegen.cpp:2753-3157): weights read from
+// `w`, one forward (+ backward and optimizer step at `lr` as given when
+// train_mode) over the model's context, the loss to *loss_out, and with
+// train_mode the updated weights to `wout` (NULL: not written back).  No LR
+// schedule and no step counter: those belong to the wrapper.
+int nsh_train_core(ns_model* m, const float* x, size_t nx, const float* y, const float* w, float* wout,
+                   float* loss_out, float lr, int train_mode) {
+  if (!m || !x || !y || !w) {
+    set_error("train_core: null argument");
+    return -1;
+  }
+  if (!m->plan->has_train) {
+    set_error("train_core: the network has no train() method");
+    return -1;
+  }
+  if (nsh_model_set_weights(m, w, m->plan->total) != 0) return -1;
+  float *dx = nullptr, *dy = nullptr;
+  if (stage_train_inputs(m, x, y, nx, &dx, &dy) != 0) return -1;
+  float* d_loss = nullptr;
+  const int rc = run_train(m, dx, nx, dy, train_mode ? lr : 0.f, train_mode != 0, &d_loss);
+  m->labels_host = nullptr;
+  if (rc != 0) return -1;
+  float loss = 0.f;
+  NSH_CHECK(hipMemcpyAsync(&loss, d_loss, sizeof(float), hipMemcpyDeviceToHost, m->stream));
+  if (sync(m) != 0) return -1;
+  if (loss_out) *loss_out = loss;
+  if (train_mode && wout && nsh_model_get_weights(m, wout, m->plan->total) != 0) return -1;
   return 0;
 }
 
@@ -1643,6 +1748,7 @@ size_t nsh_op_embedding_grad_workspace(int64_t n, int64_t V) { return embedding_
 int nsh_op_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                           void* workspace) {
   NSH_OP_REQUIRE(n >= 0 && V >= 0 && D >= 0 && (V * D == 0 || dW) && (n == 0 || (dout && idx)), "embedding_grad");
+  if (V == 0 || D == 0) return 0;  // dW is empty: no device work
   if (!workspace || launch_embedding_grad(dout, idx, dW, n, V, D, (int*)workspace, nullptr) != 0) return -1;
   NSH_OP_DONE();
 }
@@ -1753,6 +1859,15 @@ int nsh_bench_copy(const float* src, float* dst, int64_t n, int reps, double* gb
   return 0;
 }
 
+int nsh_bench_rowops(const float* idx, const float* labels, int64_t M, int64_t D, int64_t V, int64_t C, int reps,
+                     double* us) {
+  if (!idx || !labels || M <= 0 || D <= 0 || V <= 0 || C <= 0 || reps <= 0 || !us) {
+    set_error("bench_rowops: bad arguments");
+    return -1;
+  }
+  return bench_rowops(idx, labels, M, D, V, C, reps, us);
+}
+
 int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, int64_t t, float lr) {
   NSH_OP_REQUIRE(n >= 0 && (n == 0 || (w && g && m && v)), "adamw_step");
   const float b1t = 1.f - powf(0.9f, (float)t), b2t = 1.f - powf(0.999f, (float)t);
@@ -1763,8 +1878,16 @@ int nsh_op_adamw_step(float* w, const float* g, float* m, float* v, int64_t n, i
 int nsh_op_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S,
                          int64_t D, int64_t H) {
   NSH_OP_REQUIRE(S >= 0 && (S == 0 || (Q && K && V && ctx)), "attention_fwd");
-  if (launch_attention_fwd(Q, K, V, ctx, lse, S, D, H, D, nullptr) != 0) return -1;
-  NSH_OP_DONE();
+  const void* rd[3] = {Q, K, V};
+  float* pad = nullptr;  // padded copies for head sizes the tiled kernels do not take in place
+  if (S > 0 && !attention_in_place(D, H, D, rd, 3) && attention_pad_floats(S, D, H, false))
+    NSH_CHECK(hipMalloc(&pad, attention_pad_floats(S, D, H, false) * sizeof(float)));
+  const int rc = launch_attention_fwd(Q, K, V, ctx, lse, S, D, H, D, pad, nullptr);
+  const hipError_t e = hipStreamSynchronize(nullptr);
+  if (pad) hipFree(pad);
+  if (rc != 0) return -1;
+  NSH_CHECK(e);
+  return 0;
 }
 
 // workspace: delta [H*S] (rounded up to 64 floats), then dS when stored.
@@ -1784,8 +1907,16 @@ int nsh_op_attention_bwd(const float* Q, const float* K, const float* V, const f
   }
   float* delta = (float*)workspace;
   float* ds = store_ds && attention_bwd_ds_floats(S, D, H) ? delta + attn_delta_floats(S, H) : nullptr;
-  if (launch_attention_bwd(Q, K, V, O, dO, lse, delta, dQ, dK, dV, S, D, H, D, ds, nullptr) != 0) return -1;
-  NSH_OP_DONE();
+  const void* rd[5] = {Q, K, V, O, dO};
+  float* pad = nullptr;  // padded copies for head sizes the tiled kernels do not take in place
+  if (S > 0 && !attention_in_place(D, H, D, rd, 5) && attention_pad_floats(S, D, H, true))
+    NSH_CHECK(hipMalloc(&pad, attention_pad_floats(S, D, H, true) * sizeof(float)));
+  const int rc = launch_attention_bwd(Q, K, V, O, dO, lse, delta, dQ, dK, dV, S, D, H, D, ds, pad, nullptr);
+  const hipError_t e = hipStreamSynchronize(nullptr);
+  if (pad) hipFree(pad);
+  if (rc != 0) return -1;
+  NSH_CHECK(e);
+  return 0;
 }
 
 }  // extern "C"

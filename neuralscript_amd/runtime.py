@@ -83,6 +83,7 @@ def lib():
             "nsh_op_adamw_step": (ci, [vp, vp, vp, vp, i64, i64, cf]),
             "nsh_bench_mfma_peak": (ci, [ci, ci, ctypes.POINTER(ctypes.c_double)]),
             "nsh_bench_copy": (ci, [vp, vp, i64, ci, ctypes.POINTER(ctypes.c_double)]),
+            "nsh_bench_rowops": (ci, [vp, vp, i64, i64, i64, i64, ci, ctypes.POINTER(ctypes.c_double)]),
             "nsh_op_muon_multi_workspace": (sz, [ci, vp, vp]),
             "nsh_op_muon_multi": (ci, [ci, vp, vp, vp, vp, cf, vp]),
             "nsh_op_embedding": (ci, [vp, vp, vp, i64, i64, i64]),

@@ -30,6 +30,11 @@ CONFIGS = {
                    "fp32 MLP 1024->4096 GELU->4096 GELU->1024, batch 8192, N(0,1) inputs, Xavier-uniform weights"),
     "c3": Workload("c3", "c3", 16384, 0x5EED0003,
                    "fp32 Embedding(32000,1024)->Attention(1024,16)->LayerNorm, 8x2048 ids as one 16384-token sequence, N(0,0.02) weights"),
+    # not a BASELINE config: c3 with 8 heads of 128 (Attention(1024, 8)), the
+    # head size of the flash kernels' DK = 128 instantiation
+    "c3d": Workload("c3d", "c3d", 16384, 0x5EED0003,
+                    "fp32 Embedding(32000,1024)->Attention(1024,8)->LayerNorm (head size 128), c3's 16384-token "
+                    "sequence and weights"),
     "c4": Workload("c4", "c4", 65536, 0x5EED0004,
                    "fp32 top-1 MoE, 65536 tokens, d_model 1024, 64 experts (FFN 1024), Zipf(1.1) gate bias folded into Wg"),
     "c5": Workload("c5", "c5", 16384, 0x5EED0005,
@@ -78,7 +83,7 @@ def inputs(key, rows=None, in_cols=None, vocab=None, D=None):
         return synth.uniform(s, rows * 64, -1.0, 1.0)
     if key == "c2":
         return synth.normal(s, rows * 1024)
-    if key == "c3":
+    if key in ("c3", "c3d"):
         return synth.token_ids(s, rows, 32000)
     if key == "c4":
         x = synth.normal(s, rows * 1024).reshape(rows, 1024)

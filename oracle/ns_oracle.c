@@ -926,12 +926,18 @@ EXPORT int or_use_muon(int64_t r, int64_t c) {
     return r > 1 && c > 1 && (r < c ? r : c) >= 8;
 }
 
-/* Cosine-with-warmup multiplier (optim_params.hpp:54-62 / codegen.cpp:23-39),
- * for hosts that apply the schedule themselves. */
-EXPORT float or_lr_scale_cosine(int64_t step) {
-    if (step < 100) return (float)step / (float)100;
-    const int64_t end = 10000;
+/* The runtime wrapper's multiplier lr_scale (optim_params.hpp:54-62, emitted
+ * as ns_lr_schedule codegen.cpp:23-39): kind 0 constant; kind 1 linear
+ * warmup over `warmup` steps, then a half cosine to `min_factor` at `total`. */
+EXPORT float or_lr_scale(int kind, int64_t warmup, int64_t total, float min_factor, int64_t step) {
+    if (kind == 0) return 1.0f;
+    if (step < warmup) return warmup > 0 ? (float)step / (float)warmup : 1.0f;
+    const int64_t end = total > warmup ? total : warmup + 1;
     const int64_t s = step >= end ? end : step;
-    const float t = (float)(s - 100) / (float)(end - 100);
-    return 0.05f + 0.5f * (1.0f - 0.05f) * (1.0f + cosf(3.14159265f * t));
+    const float t = (float)(s - warmup) / (float)(end - warmup);
+    return min_factor + 0.5f * (1.0f - min_factor) * (1.0f + cosf(3.14159265f * t));
 }
+
+/* Cosine-with-warmup at optim_params.hpp's constants (warmup 100, total
+ * 10000, floor 0.05), for hosts that apply the schedule themselves. */
+EXPORT float or_lr_scale_cosine(int64_t step) { return or_lr_scale(1, 100, 10000, 0.05f, step); }

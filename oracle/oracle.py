@@ -112,6 +112,7 @@ def _load(which):
             "or_adamw_step": (None, [_f32p, _f32p, _f32p, _f32p, sz, i64, cf]),
             "or_use_muon": (ci, [i64, i64]),
             "or_lr_scale_cosine": (cf, [i64]),
+            "or_lr_scale": (cf, [ci, i64, i64, cf, i64]),
             "or_set_mgs_partials": (None, [ci]),
         }
         if which == "reference":
@@ -319,6 +320,30 @@ def lr_scale_cosine(step):
     return float(_load("oracle").or_lr_scale_cosine(step))
 
 
+def lr_scale(sched, step):
+    """The multiplier of schedule `sched` (Net.lr_schedule) at wrapper step
+    `step` (optim_params.hpp:54-62)."""
+    return float(_load("oracle").or_lr_scale(sched["kind"], sched["warmup"], sched["total"],
+                                             ctypes.c_float(sched["min"]), step))
+
+
+def parse_lr_schedule(text):
+    """The `// ns.lr_schedule <kind> warmup=W total=T min=F` line of the IR
+    text (the reference's compiled-in optim::kLRSchedule and its constants,
+    optim_params.hpp:36-52); absent: the constant schedule."""
+    out = {"kind": 0, "warmup": 100, "total": 10000, "min": 0.05}
+    for raw in text.splitlines():
+        line = raw.strip()
+        if not line.startswith("// ns.lr_schedule"):
+            continue
+        toks = line[len("// ns.lr_schedule"):].split()
+        out["kind"] = {"constant": 0, "cosine_warmup": 1}[toks[0]]
+        for t in toks[1:]:
+            k, v = t.split("=", 1)
+            out[k] = float(np.float32(v)) if k == "min" else int(v)
+    return out
+
+
 # ---------------------------------------------------------------------------
 # IR text (nsc --mlir) parsing
 # ---------------------------------------------------------------------------
@@ -446,6 +471,7 @@ class Net:
 
     def __init__(self, ir_text):
         self.funcs = parse_ir(ir_text)
+        self.lr_schedule = parse_lr_schedule(ir_text)
         self.fwd = next((f for f in self.funcs if not f.is_train), None)
         self.train = next((f for f in self.funcs if f.is_train), None)
         if self.fwd is None:
@@ -948,10 +974,12 @@ class Model:
         return buf[self.net.fwd.ret].copy()
 
     def train_step(self, x, labels, lr, record=None):
-        """ns_runtime_train_step with the compiled-in constant schedule
-        (multiplier 1.0, codegen.cpp:2639-2642)."""
+        """ns_runtime_train_step: the compiled-in schedule's multiplier at the
+        model's step counter, which then advances (codegen.cpp:2636-2644;
+        the reference compiles the constant schedule, multiplier 1)."""
+        step = self.lr_step
         self.lr_step += 1
-        self._lr = np.float32(lr) * np.float32(1.0)
+        self._lr = np.float32(lr) * np.float32(lr_scale(self.net.lr_schedule, step))
         _, loss = self._run(self.net.train, f32(x).ravel(), f32(labels).ravel(), True, record)
         return np.float32(loss)
 

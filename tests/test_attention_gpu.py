@@ -25,8 +25,14 @@ def core_ref(Q, K, V, S, D, H):
     return out
 
 
-@pytest.mark.parametrize("S,D,H", [(1, 64, 1), (100, 128, 2), (333, 64, 1), (1024, 1024, 16), (300, 64, 2),
-                                   (257, 16, 2), (90, 64, 8), (2048, 512, 8), (100, 128, 1), (77, 192, 2)])
+# Head sizes: 64 and 32 and 128 in place; 8, 16, 48, 80, 96, 7 (rows not
+# 16-byte aligned) on copies padded with zero columns to 32, 64 or 128.
+SHAPES_FWD = [(1, 64, 1), (100, 128, 2), (333, 64, 1), (1024, 1024, 16), (300, 64, 2), (257, 16, 2), (90, 64, 8),
+              (2048, 512, 8), (100, 128, 1), (77, 192, 2), (2048, 1024, 8), (333, 256, 2), (300, 96, 2),
+              (257, 64, 4), (130, 160, 2), (77, 21, 3), (64, 128, 4)]
+
+
+@pytest.mark.parametrize("S,D,H", SHAPES_FWD)
 def test_attention_core_matches_float64(S, D, H):
     print(f"attention core S={S} D={D} H={H}", flush=True)
     Q, K, V = (synth.normal(S * 10 + i, S * D, 1.0) for i in range(3))
@@ -58,13 +64,14 @@ def core_bwd_ref(Q, K, V, dO, S, D, H):
 
 @pytest.mark.parametrize("S,D,H", [(64, 128, 2), (128, 128, 2), (192, 128, 2), (100, 128, 2), (256, 64, 2),
                                    (130, 64, 2), (90, 64, 8), (1024, 512, 8), (2048, 512, 8), (100, 128, 1),
-                                   (77, 192, 2)])
+                                   (77, 192, 2), (2048, 1024, 8), (333, 256, 2), (320, 256, 2), (300, 96, 2),
+                                   (257, 64, 4), (130, 160, 2), (77, 21, 3)])
 @pytest.mark.parametrize("store_ds", [0, 1])
 def test_attention_core_backward_matches_float64(S, D, H, store_ds):
-    """Flash backward (head size 32/64: key-parallel dK/dV pass, then dQ
-    either from the stored dS or from a query-parallel pass recomputing S and
-    dP) and the small-head kernels, vs the float64 gradient at the fp32 bar
-    |d| <= 1e-5 + 1e-4 |ref| (measured worst: 0.05 of it)."""
+    """Flash backward (key-parallel dK/dV pass, then dQ either from the
+    stored dS or from a query-parallel pass recomputing S and dP) at head
+    sizes 32, 64, 128 in place and the others padded, vs the float64
+    gradient at the fp32 bar |d| <= 1e-5 + 1e-4 |ref|."""
     print(f"attention backward S={S} D={D} H={H} store_ds={store_ds}", flush=True)
     Q, K, V, dO = (synth.normal(S * 20 + i, S * D, 1.0) for i in range(4))
     dQ_, dK_, dV_ = (DA(S * D) for _ in range(3))
@@ -79,6 +86,15 @@ def test_attention_core_backward_matches_float64(S, D, H, store_ds):
         print(f"  {name}: violation at the plain bar x{helpers.violation(got.to_host(), ref):.3g}, "
               f"max|ref| {float(np.abs(ref).max()):.3g}")
         helpers.assert_close(got.to_host(), ref, f"attention {name} S={S} D={D} H={H} ds={store_ds}")
+
+
+@pytest.mark.parametrize("S,D,H", [(64, 320, 2), (64, 1024, 4)])
+def test_attention_head_size_above_128_is_refused(S, D, H):
+    """Head sizes above 128 have no tiled kernel: -1 and a message, before any
+    device work."""
+    Q = DA(S * D)
+    rc = runtime.lib().nsh_op_attention_fwd(Q.ptr, Q.ptr, Q.ptr, Q.ptr, None, S, D, H)
+    assert rc == -1 and "above 128" in runtime.last_error()
 
 
 def test_attention_layer_matches_oracle():
@@ -130,3 +146,44 @@ def test_c3_full_size_rows_match_oracle():
     att = oracle.attention_fwd_rows(emb, Wq, Wk, Wv, Wo, rows, 16384, 1024, 16)
     ref = oracle.layernorm(att, 1024).reshape(len(rows), 1024)
     helpers.assert_close(out[rows], ref, "c3 rows")
+
+
+@pytest.mark.parametrize("rows", [2048, 333])
+def test_c3_with_head_size_128_matches_oracle(rows):
+    """c3d (c3's network with Attention(1024, 8): head size 128, the flash
+    kernels' DK = 128 instantiation) against the oracle at 2048 and 333
+    tokens, all rows."""
+    print(f"c3d S={rows}", flush=True)
+    ir = helpers.ir_text("c3d")
+    w = helpers.net_weights("c3d", rows, std=0.1)
+    net = oracle.Net(ir)
+    x = helpers.net_inputs(net, "c3d", rows, rows)
+    ref = oracle.Model(net, w).eval_infer(x)
+    lib = runtime.net_lib("c3d")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x)
+    lib.free(m)
+    helpers.assert_close(out, ref, f"c3d S={rows}")
+
+
+def test_c3d_full_size_rows_match_oracle():
+    """c3d at c3's full size (16384 tokens as one sequence, 8 heads of 128):
+    24 query rows recomputed by the oracle (full K/V) and their LN."""
+    print("c3d full size", flush=True)
+    ir = helpers.ir_text("c3d")
+    plan = runtime.Plan(ir)
+    w = workloads.weights("c3d", plan.layout(), workloads.ir_shapes(ir))
+    x = workloads.inputs("c3d")
+    lib = runtime.net_lib("c3d")
+    m = lib.init(w)
+    out = lib.eval_infer(m, x).reshape(16384, 1024)
+    lib.free(m)
+    assert np.isfinite(out).all()
+    net = oracle.Net(ir)
+    o = net.offsets
+    emb = oracle.embedding(w[: 32000 * 1024], x, 32000, 1024)
+    Wq, Wk, Wv, Wo = (w[o[n]: o[n] + 1024 * 1024] for n in ("attn_q_w", "attn_k_w", "attn_v_w", "attn_o_w"))
+    rows = np.unique(np.linspace(0, 16383, 24).astype(np.int64))
+    att = oracle.attention_fwd_rows(emb, Wq, Wk, Wv, Wo, rows, 16384, 1024, 8)
+    ref = oracle.layernorm(att, 1024).reshape(len(rows), 1024)
+    helpers.assert_close(out[rows], ref, "c3d rows")

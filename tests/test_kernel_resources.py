@@ -19,9 +19,9 @@ import pytest
 from neuralscript_amd import build
 
 SOURCES = ["gemm.hip", "attention.hip", "optim.hip", "rowops.hip", "moe.hip", "movement.hip"]
-# Generic-head-dimension attention kernels keep per-thread rows of any length
-# in private arrays by design; they serve shapes the tiled kernels do not.
-ALLOWED = ("attention_fwd_small_kernel", "attn_bwd_small_q_kernel", "attn_bwd_small_kv_kernel")
+# Kernels allowed a private segment: none (every attention head size runs on
+# the tiled MFMA kernels, padded where needed).
+ALLOWED = ()
 
 pytestmark = pytest.mark.skipif(shutil.which("hipcc") is None, reason="hipcc not installed")
 

@@ -71,13 +71,16 @@ def test_activation_backward(act):
 @pytest.mark.parametrize("n,V,D,mode", [(16384, 8192, 512, "uniform"), (3000, 40, 16, "uniform"),
                                         (700, 50, 33, "same"), (500, 1000, 8, "edge"),
                                         (4096, 64, 512, "same"), (20000, 300, 1024, "skew"),
-                                        (5000, 20000, 64, "uniform")])
+                                        (5000, 20000, 64, "uniform"), (32768, 8191, 1000, "uniform"),
+                                        (0, 37, 8, "uniform"), (40000, 8192, 512, "uniform"),
+                                        (50000, 300, 64, "skew"), (33000, 17, 20, "same")])
 def test_embedding_grad_is_bit_exact(n, V, D, mode):
-    """Row sums in ascending token order: float4 columns (D % 4 == 0: one,
-    two or four float4 per lane) or scalar ones; short segments sorted per
-    thread, long ones (one row taking every token; several heavy rows in one
-    block under skewed ids) by the workgroup; V above 8192 takes the scan's
-    looping path."""
+    """Row sums in ascending token order, float4 columns (D % 4 == 0: one,
+    two or four float4 per lane) or scalar ones.  Up to 32768 tokens one
+    launch walks per-row token bitmaps (32768: the bitmaps fill 64 KB of LDS;
+    no tokens: every row zero); beyond, the counting-sort path: short
+    segments sorted per thread, long ones (one row taking every token;
+    several heavy rows in one block under skewed ids) by the workgroup."""
     print(f"embedding_grad n={n} V={V} D={D} {mode}", flush=True)
     if mode == "same":
         idx = np.full(n, 3.0, np.float32)   # one row takes every token
