@@ -64,10 +64,19 @@ class CopyPool {
     size_t n = 0;
     int parts = 1;
   };
+  // Helper threads that cannot be created (a process or thread limit) are
+  // simply fewer helpers: copies split over the threads that exist, down to
+  // the calling thread alone, so no exception leaves the C ABI.
   CopyPool() {
     const unsigned hw = std::thread::hardware_concurrency();
     const int helpers = hw > 1 ? (int)std::min(4u, hw - 1) : 0;
-    for (int i = 0; i < helpers; i++) th_.emplace_back([this, i] { worker(i + 1); });
+    for (int i = 0; i < helpers; i++) {
+      try {
+        th_.emplace_back([this, i] { worker(i + 1); });
+      } catch (const std::exception&) {
+        break;
+      }
+    }
   }
   // part p of the job: 64-byte aligned pieces of ceil(n / parts)
   static void run(const Job& j, int p) {

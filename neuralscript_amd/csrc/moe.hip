@@ -31,6 +31,9 @@ namespace {
 constexpr int kTok = 64;   // tokens per router workgroup
 constexpr int kKS = 32;    // k slab
 constexpr int kBlk = 256;  // tokens per dispatch block
+// Experts of one MoE layer: the scan's per-expert tables (3 E + 2 ints) sit
+// in 64 KB of dynamic LDS.
+constexpr int kMaxExperts = 4096;
 
 // exp(x) correctly rounded to float (double evaluation, one rounding).
 __device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
@@ -200,6 +203,78 @@ __global__ __launch_bounds__(256) void moe_router_tok_kernel(const float* __rest
   prob[tok] = (sum > 0.f && b >= 0) ? bv / sum : 0.f;
 }
 
+// Router logits for any number of experts: workgroup (token tile, expert
+// tile) computes 64 tokens x 64 experts, each logit a sequential-k fp32 sum
+// with contraction off (the arithmetic of moe_router_kernel), into logits.
+__global__ __launch_bounds__(256) void moe_logits_kernel(const float* __restrict__ x, const float* __restrict__ Wg,
+                                                         float* __restrict__ logits, int M, int D, int E) {
+#pragma clang fp contract(off)
+  __shared__ float xs[kTok][kKS + 1];
+  __shared__ float ws[kKS][64];
+  const int t = threadIdx.x;
+  const int el = t & 63, tg = t >> 6;  // expert lane, token group (16 tokens)
+  const int tok0 = blockIdx.x * kTok, eb = blockIdx.y * 64;
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = 0.f;
+  for (int k0 = 0; k0 < D; k0 += kKS) {
+    for (int i = t; i < kTok * kKS; i += 256) {
+      const int r = i / kKS, c = i % kKS;
+      const int tok = tok0 + r, k = k0 + c;
+      xs[r][c] = (tok < M && k < D) ? x[(int64_t)tok * D + k] : 0.f;
+    }
+    for (int i = t; i < kKS * 64; i += 256) {
+      const int r = i / 64, c = i % 64;
+      const int k = k0 + r;
+      ws[r][c] = (k < D && eb + c < E) ? Wg[(int64_t)k * E + eb + c] : 0.f;
+    }
+    __syncthreads();
+    const int kn = min(kKS, D - k0);
+    for (int kk = 0; kk < kn; kk++) {
+      const float w = ws[kk][el];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float prod = xs[tg * 16 + i][kk] * w;
+        acc[i] = acc[i] + prod;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const int tok = tok0 + tg * 16 + i;
+    if (tok < M && eb + el < E) logits[(int64_t)tok * E + eb + el] = acc[i];
+  }
+}
+
+// Routing from stored logits, one thread per token, experts in ascending
+// order (first strict maximum of the exp'd values wins), as the router
+// kernels route.
+__global__ __launch_bounds__(256) void moe_route_logits_kernel(const float* __restrict__ logits,
+                                                               const uint8_t* __restrict__ active,
+                                                               int* __restrict__ best, float* __restrict__ prob, int M,
+                                                               int E) {
+  const int tok = blockIdx.x * 256 + threadIdx.x;
+  if (tok >= M) return;
+  const float* l = logits + (int64_t)tok * E;
+  float mx = -1.0e30f;
+  for (int e = 0; e < E; e++)
+    if ((!active || active[e]) && l[e] > mx) mx = l[e];
+  float sum = 0.f, bv = 0.f;
+  int b = -1;
+  for (int e = 0; e < E; e++) {
+    if (active && !active[e]) continue;
+    const float v = exp_rn(l[e] - mx);
+    sum = sum + v;
+    if (b < 0 || v > bv) {
+      b = e;
+      bv = v;
+    }
+  }
+  best[tok] = b;
+  prob[tok] = (sum > 0.f && b >= 0) ? bv / sum : 0.f;
+}
+
 // In-block rank of each token among same-expert tokens, and block counts.
 __global__ __launch_bounds__(kBlk) void moe_rank_kernel(const int* __restrict__ best, int* __restrict__ rank,
                                                         int* __restrict__ bcount, int M, int E) {
@@ -332,11 +407,15 @@ __global__ __launch_bounds__(256) void moe_scan_lds_kernel(int* __restrict__ bco
 }
 
 // Expert segments, per-block offsets (in place over bcount) and the
-// (expert, m-tile) list.  One workgroup; thread e owns expert e.
+// (expert, m-tile) list.  One workgroup; thread t owns experts t, t + 256,
+// ...; the per-expert tables live in dynamic LDS (3 E + 2 ints).
 __global__ __launch_bounds__(256) void moe_scan_kernel(int* __restrict__ bcount, int* __restrict__ seg,
                                                        int* __restrict__ tiles, int* __restrict__ ntiles, int nblk,
                                                        int E, int bm) {
-  __shared__ int tot[256], base[257], tb[257];
+  extern __shared__ int scan_tab[];
+  int* tot = scan_tab;
+  int* base = scan_tab + E;
+  int* tb = base + E + 1;
   const int t = threadIdx.x;
   for (int e = t; e < E; e += 256) {
     int c = 0;
@@ -406,13 +485,19 @@ size_t moe_work_ints(int64_t M, int64_t E) {
 int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
                      int64_t E, hipStream_t s) {
   if (M <= 0) return 0;
-  if (E > 256 || M > INT32_MAX / 2) {
-    set_error("moe: more than 256 experts or too many tokens");
+  if (E > kMaxExperts || M > INT32_MAX / 2) {
+    set_error("moe: more than " + std::to_string(kMaxExperts) + " experts or too many tokens");
     return -1;
   }
   const int m = (int)M, d = (int)D, e = (int)E;
   const bool tok_path = E <= 64 && D % 4 == 0 && ((uintptr_t)x & 15) == 0;
-  if (tok_path) {
+  if (E > 256) {  // logits by expert tiles, then routing from them
+    hipLaunchKernelGGL(moe_logits_kernel, dim3((unsigned)ceil_div(M, kTok), (unsigned)ceil_div(E, 64)), dim3(256), 0,
+                       s, x, Wg, w.logits, m, d, e);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(moe_route_logits_kernel, dim3((unsigned)ceil_div(M, 256)), dim3(256), 0, s, w.logits, active,
+                       w.best, w.prob, m, e);
+  } else if (tok_path) {
     const dim3 g((unsigned)ceil_div(M, kRT));
 #define NSH_ROUTER(EG_)                                                                                      \
   if (E == 4 * EG_)                                                                                          \
@@ -436,10 +521,11 @@ int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, con
   const int nblk = (int)ceil_div(M, kBlk);
   hipLaunchKernelGGL(moe_rank_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, m, e);
   NSH_LAUNCHED();
-  if ((int64_t)nblk * E <= kScanLds)
+  if ((int64_t)nblk * E <= kScanLds && E <= 256)
     hipLaunchKernelGGL(moe_scan_lds_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
   else
-    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), (3 * E + 2) * sizeof(int), s, w.bcount, w.seg, w.tiles,
+                       w.ntiles, nblk, e, 128);
   NSH_LAUNCHED();
   hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, w.perm, m, e);
   NSH_LAUNCHED();
@@ -497,8 +583,9 @@ int launch_moe_experts(const float* x, const float* We1, const float* We2, const
 // segment as the contraction (dWe1, dWe2).
 // ============================================================================
 
-// One wave per routed (expert-sorted) row.
-template <int EPT>
+// One wave per routed (expert-sorted) row; the routing probabilities are
+// recomputed from the logits where each is used (p_b by every lane, p_e by
+// the lane writing dg_e), all by the same expression.
 __global__ __launch_bounds__(256) void moe_bwd_rows_kernel(const float* __restrict__ pre, const float* __restrict__ dpre2,
                                                            const float* __restrict__ logits,
                                                            const uint8_t* __restrict__ active,
@@ -521,16 +608,11 @@ __global__ __launch_bounds__(256) void moe_bwd_rows_kernel(const float* __restri
   }
   mx = __shfl(mx, 0, 64);
   sum = __shfl(sum, 0, 64);
-  float pe[EPT];
-  float pb = 0.f;
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int e = lane + 64 * j;
-    const bool live = e < E && (!active || active[e]);
-    pe[j] = (live && sum > 0.f) ? exp_rn(l[e] - mx) / sum : 0.f;
-    if (e == b) pb = pe[j];
-  }
-  pb = wave_sum(pb);  // exactly one lane holds it
+  auto prob_of = [&](int e) {
+    const bool live = e >= 0 && e < E && (!active || active[e]);
+    return (live && sum > 0.f) ? exp_rn(l[e] - mx) / sum : 0.f;
+  };
+  const float pb = prob_of(b);
   const float* u = pre + pos * H;
   const float* d2 = dpre2 + pos * H;
   float* dh = dH + pos * H;
@@ -546,11 +628,7 @@ __global__ __launch_bounds__(256) void moe_bwd_rows_kernel(const float* __restri
   }
   dpb = wave_sum(dpb);
   const float sd = dpb * pb;
-#pragma unroll
-  for (int j = 0; j < EPT; j++) {
-    const int e = lane + 64 * j;
-    if (e < E) dg[(int64_t)tok * E + e] = pe[j] * ((e == b ? dpb : 0.f) - sd);
-  }
+  for (int e = lane; e < E; e += 64) dg[(int64_t)tok * E + e] = prob_of(e) * ((e == b ? dpb : 0.f) - sd);
 }
 
 __global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ perm,
@@ -603,15 +681,8 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
   hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)ceil_div(M * E, 256)), dim3(256), 0, s, b.dg, M * E);
   NSH_LAUNCHED();
   const dim3 rg((unsigned)ceil_div(M, 4));
-  if (E <= 64)
-    hipLaunchKernelGGL(moe_bwd_rows_kernel<1>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
-                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
-  else if (E <= 128)
-    hipLaunchKernelGGL(moe_bwd_rows_kernel<2>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
-                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
-  else
-    hipLaunchKernelGGL(moe_bwd_rows_kernel<4>, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
-                       nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
+  hipLaunchKernelGGL(moe_bwd_rows_kernel, rg, dim3(256), 0, s, w.pre, b.dpre2, w.logits, active, w.perm, w.best,
+                     nrows, b.dH, b.hp, b.dg, (int)H, (int)E);
   NSH_LAUNCHED();
   // dx = dg Wg^T, then += dH We1[e]^T scattered back to token order
   if (dx) {

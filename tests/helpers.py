@@ -37,6 +37,12 @@ def net_weights(name, seed, std=0.2):
     return workloads.generic_weights(layout(name), shapes(name), seed, std)
 
 
+def net_weights_for(net, seed, std=0.2):
+    """net_weights for an oracle.Net that is not a bundled plan."""
+    lay = [(n, net.offsets[n], r * c) for n, r, c in net.weights]
+    return workloads.generic_weights(lay, dict(net.shape), seed, std)
+
+
 def net_inputs(net, name, seed, M):
     """Token ids for embedding-first nets, N(0,1) rows for MoE-first nets,
     U[-1,1] rows otherwise."""

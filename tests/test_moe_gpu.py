@@ -69,7 +69,8 @@ def test_moe_lifecycle_matches_reference_fixture():
 
 @pytest.mark.parametrize("M,D,E,H,mask", [(1000, 64, 8, 96, None), (3000, 128, 64, 64, None),
                                           (777, 64, 16, 32, "some"), (513, 32, 130, 16, None),
-                                          (600, 32, 256, 16, "some")])
+                                          (600, 32, 256, 16, "some"), (400, 32, 300, 8, "some"),
+                                          (300, 16, 1000, 4, None)])
 def test_moe_routing_is_bit_exact(M, D, E, H, mask):
     print(f"moe routing M={M} D={D} E={E} H={H}", flush=True)
     ir = ("ns.func @MOE {\n"
@@ -330,3 +331,35 @@ def test_moe_backward_at_production_shape():
             bad.append((ins.op, viol, floor))
     model.free()
     assert not bad, bad
+
+
+@pytest.mark.parametrize("E,rows", [(300, 300), (1000, 257)])
+def test_moe_training_step_with_many_experts(E, rows):
+    """More than 256 experts (the router's logits by expert tiles, routing
+    from them, the dispatch scan's tables in dynamic LDS, the backward's
+    routing probabilities per lane): moet's network with E experts (three
+    quarters live), one training step against the oracle -- expert choices
+    bit-exact, every MoE gradient and the loss at the fp32 bar."""
+    print(f"moe training E={E} rows={rows}", flush=True)
+    ir = (helpers.ir_text("moet").replace("Tensor[32, 8]", f"Tensor[32, {E}]")
+          .replace("Tensor[8, 1536]", f"Tensor[{E}, 1536]").replace("experts=8", f"experts={E}")
+          .replace("initial=6", f"initial={3 * E // 4}"))
+    net = oracle.Net(ir)
+    assert net.moe["E"] == E and net.moe["K0"] == 3 * E // 4
+    seed = 700 + E
+    x = helpers.net_inputs(net, "moet", seed, rows)
+    y = helpers.net_labels(net, seed, rows)
+    w = helpers.net_weights_for(net, seed)
+    om = oracle.Model(net, w)
+    rec = {}
+    ref_loss = om.train_step(x, y, 0.02, rec)
+    model = runtime.Model(runtime.Plan(ir), w)
+    loss = model.train_step(x, y, 0.02)
+    best, _, _ = model.last_routing(rows, E)
+    assert np.array_equal(best, rec["moe_best"]), "expert choice differs"
+    helpers.assert_close(np.float32(loss), ref_loss, "loss")
+    for ins in net.train.instrs:
+        if ins.op.startswith("ns.grad.moe."):
+            ref = rec["buf"][ins.result]
+            helpers.assert_close(model.read_value(ins.result, ref.size), ref, f"{ins.op} E={E}")
+    model.free()
