@@ -26,12 +26,20 @@
 // vectors over the 1024 threads according to its own matrix's length.  Vectors live
 // contiguously in a work buffer T[C][R] (a transpose of g when r >= c).
 // Vectors longer than kMaxPanelR take the sliced path: every vector is cut
-// into slices of kSliceLen elements, one workgroup per slice holds its slice
-// of every vector, and one launch per column j turns column j's per-slice
-// partial sums (written by the previous launch) into |v_j| and the dots,
-// normalises q_j, projects it out of every later vector's slice in order,
-// and writes the partial sums of column j + 1 -- one grid-wide exchange per
-// column.
+// into slices of kSliceLen elements, one workgroup per slice, and the
+// columns go in panels of kSlicePanel.  Inside a panel, one launch per
+// column j turns column j's per-slice partial sums (written by the previous
+// launch) into |v_j| and the dots, normalises q_j, projects it out of the
+// panel's later vectors in order and writes the partial sums of column j + 1
+// (MGS, one grid-wide exchange per column).  The finished panel then
+// projects out of every later vector at once, block Gram-Schmidt: the raw
+// dots q_k . v_c of each panel vector with each later vector (per slice, then
+// summed in a fixed order), then v_c -= sum_k (q_k . v_c) q_k, k ascending --
+// each later vector is streamed three times per panel instead of twice per
+// column.  Only the order of the cross-panel projections differs from the
+// reference's MGS (the dots are taken from the vector before the panel), so
+// vectors well inside the gradient's span get the same q; nearly dependent
+// ones normalise rounding residue either way.
 #include "common.h"
 #include "kernels.h"
 
@@ -42,6 +50,7 @@ constexpr int kSliceThreads = 256;                        // sliced path: thread
 constexpr int kSliceEPT = 8;                              // elements of a vector per thread
 constexpr int kSliceLen = kSliceThreads * kSliceEPT;      // elements per slice
 constexpr int kSliceBatch = 8;                            // later vectors per block reduction
+constexpr int kSlicePanel = 8;                            // columns per panel of the sliced path
 constexpr int kPB = 8;   // panel width (vectors per workgroup, panel path)
 // Panel path: 8 waves of up to 16 elements per vector a thread.  Fewer,
 // fuller waves keep the block reductions of the lead chain short: every wave
@@ -208,35 +217,33 @@ __device__ __forceinline__ float slice_total(const float* __restrict__ p, int ns
   return wave_sum(a);
 }
 
-// One column step of the sliced path over every long matrix (R >
-// kMaxPanelR); j = -1 only writes column 0's partials.  red[2][C][nsl]:
-// launch j reads buffer j & 1 and writes buffer (j + 1) & 1.  The dots use
-// the unnormalised v_j, dot_c = (v_j . v_c) / |v_j|, which equals q_j . v_c
-// up to rounding; q_j itself is v_j / |v_j| element by element, as in the
-// reference, and so is each projection v_c -= dot_c q_j.
-__global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat* __restrict__ mats, int nmat, int j) {
-  __shared__ float red[4][kSliceBatch];
-  int b = blockIdx.x, mi = 0;
-  for (; mi < nmat; mi++) {
+// The workgroup's long matrix (R > kMaxPanelR) and slice of it; false past
+// the last long matrix's slices.
+__device__ __forceinline__ bool slice_of(const MuonMat* __restrict__ mats, int nmat, int& mi, int& b) {
+  b = blockIdx.x;
+  for (mi = 0; mi < nmat; mi++) {
     const int n = mats[mi].R > kMaxPanelR ? mgs_slices(mats[mi].R) : 0;
-    if (b < n) break;
+    if (b < n) return true;
     b -= n;
   }
-  if (mi >= nmat) return;
-  const MuonMat& M = mats[mi];
-  const int C = M.C, R = M.R, nsl = mgs_slices(R);
-  if (j >= C) return;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  gfloat* __restrict__ T = as_global(M.T);
-  const float* __restrict__ Pin = M.red + (size_t)(j & 1) * C * nsl;
-  float* __restrict__ Pout = M.red + (size_t)((j + 1) & 1) * C * nsl;
-  const bool vec = R % 4 == 0 && (reinterpret_cast<uintptr_t>(M.T) & 15) == 0;
-  const int64_t s0 = (int64_t)b * kSliceLen;
-  // element e of this thread's share of the slice
-  auto at = [&](int e) -> int64_t {
+  return false;
+}
+
+// A thread's share of one slice of the vectors T[c][0..R): kSliceEPT
+// elements, float4 groups when the rows allow (R % 4 == 0, 16-byte aligned).
+struct SliceIO {
+  gfloat* __restrict__ T;
+  int R;
+  bool vec;
+  int64_t s0;
+  int t;
+  __device__ SliceIO(const MuonMat& M, int b)
+      : T(as_global(M.T)), R(M.R), vec(M.R % 4 == 0 && (reinterpret_cast<uintptr_t>(M.T) & 15) == 0),
+        s0((int64_t)b * kSliceLen), t(threadIdx.x) {}
+  __device__ int64_t at(int e) const {
     return vec ? s0 + 4 * (t + kSliceThreads * (e >> 2)) + (e & 3) : s0 + t + kSliceThreads * e;
-  };
-  auto load = [&](int c, float (&x)[kSliceEPT]) {
+  }
+  __device__ void load(int c, float (&x)[kSliceEPT]) const {
     const gfloat* row = T + (int64_t)c * R;
     if (vec) {
 #pragma unroll
@@ -250,8 +257,8 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
 #pragma unroll
       for (int e = 0; e < kSliceEPT; e++) x[e] = at(e) < R ? row[at(e)] : 0.f;
     }
-  };
-  auto store = [&](int c, const float (&x)[kSliceEPT]) {
+  }
+  __device__ void store(int c, const float (&x)[kSliceEPT]) const {
     gfloat* row = T + (int64_t)c * R;
     if (vec) {
 #pragma unroll
@@ -264,25 +271,53 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
       for (int e = 0; e < kSliceEPT; e++)
         if (at(e) < R) row[at(e)] = x[e];
     }
-  };
+  }
+};
+
+// Workspace of a long matrix (M.red): column partials [2][C][nsl], the
+// panel's raw dots per slice [kSlicePanel][C][nsl], and their totals
+// [kSlicePanel][C].
+__device__ __forceinline__ float* slice_dots(const MuonMat& M) { return M.red + (size_t)2 * M.C * mgs_slices(M.R); }
+__device__ __forceinline__ float* slice_dot_totals(const MuonMat& M) {
+  return slice_dots(M) + (size_t)kSlicePanel * M.C * mgs_slices(M.R);
+}
+
+// One column step of the sliced path inside a panel ending at column cend,
+// over every long matrix; j = -1 only writes column 0's partials.
+// Column partials: launch j reads buffer j & 1 and writes buffer (j + 1) & 1.
+// The dots use the unnormalised v_j, dot_c = (v_j . v_c) / |v_j|, which
+// equals q_j . v_c up to rounding; q_j itself is v_j / |v_j| element by
+// element, as in the reference, and so is each projection v_c -= dot_c q_j.
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat* __restrict__ mats, int nmat, int j,
+                                                                  int cend) {
+  __shared__ float red[4][kSliceBatch];
+  int mi, b;
+  if (!slice_of(mats, nmat, mi, b)) return;
+  const MuonMat& M = mats[mi];
+  const int C = M.C, nsl = mgs_slices(M.R), ce = min(C, cend);
+  if (j >= C) return;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const float* __restrict__ Pin = M.red + (size_t)(j & 1) * C * nsl;
+  float* __restrict__ Pout = M.red + (size_t)((j + 1) & 1) * C * nsl;
+  const SliceIO io(M, b);
 
   float q[kSliceEPT], nrm = 1.f;
   if (j >= 0) {
     nrm = sqrtf(slice_total(Pin + (size_t)j * nsl, nsl)) + 1e-30f;
     const float rn = 1.f / nrm;
-    load(j, q);
+    io.load(j, q);
 #pragma unroll
     for (int e = 0; e < kSliceEPT; e++) q[e] = div_shared(q[e], nrm, rn);
-    store(j, q);
+    io.store(j, q);
   }
   float piv[kSliceEPT];
-  for (int c0 = j + 1; c0 < C; c0 += kSliceBatch) {
-    const int nb = min(kSliceBatch, C - c0);
+  for (int c0 = j + 1; c0 < ce; c0 += kSliceBatch) {
+    const int nb = min(kSliceBatch, ce - c0);
     float x[kSliceBatch][kSliceEPT], d[kSliceBatch];
 #pragma unroll
     for (int u = 0; u < kSliceBatch; u++) {
       if (u < nb) {
-        load(c0 + u, x[u]);
+        io.load(c0 + u, x[u]);
       } else {
 #pragma unroll
         for (int e = 0; e < kSliceEPT; e++) x[u][e] = 0.f;
@@ -295,14 +330,14 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
         if (u >= nb) break;
 #pragma unroll
         for (int e = 0; e < kSliceEPT; e++) x[u][e] -= d[u] * q[e];
-        store(c0 + u, x[u]);
+        io.store(c0 + u, x[u]);
       }
     }
     if (c0 == j + 1) {
 #pragma unroll
       for (int e = 0; e < kSliceEPT; e++) piv[e] = x[0][e];
     }
-    // partial sums of column j + 1 over this slice: v_{j+1} . v_c, c >= j + 1
+    // partial sums of column j + 1 over this slice: v_{j+1} . v_c, j + 1 <= c < ce
 #pragma unroll
     for (int u = 0; u < kSliceBatch; u++) {
       float a = 0.f;
@@ -313,6 +348,129 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
     if (lane == 0) {
 #pragma unroll
       for (int u = 0; u < kSliceBatch; u++) red[w][u] = d[u];
+    }
+    __syncthreads();
+    if (t < nb) Pout[(size_t)(c0 + t) * nsl + b] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    __syncthreads();
+  }
+}
+
+// The finished panel [j0, j0 + kSlicePanel) against every later vector:
+// per slice, the raw dots q_k . v_c of each panel vector k with each vector
+// c >= j0 + kSlicePanel, kDotBatch vectors at a time.
+constexpr int kDotBatch = 4;
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_dots_kernel(const MuonMat* __restrict__ mats, int nmat,
+                                                                       int j0) {
+  __shared__ float red[4][kDotBatch * kSlicePanel];
+  int mi, b;
+  if (!slice_of(mats, nmat, mi, b)) return;
+  const MuonMat& M = mats[mi];
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
+  if (j1 >= C) return;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const SliceIO io(M, b);
+  float* __restrict__ pd = slice_dots(M);
+  float q[kSlicePanel][kSliceEPT];
+#pragma unroll
+  for (int k = 0; k < kSlicePanel; k++) io.load(j0 + k, q[k]);
+  for (int c0 = j1; c0 < C; c0 += kDotBatch) {
+    const int nb = min(kDotBatch, C - c0);
+    float x[kDotBatch][kSliceEPT];
+#pragma unroll
+    for (int u = 0; u < kDotBatch; u++) {
+      if (u < nb) {
+        io.load(c0 + u, x[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) x[u][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDotBatch; u++)
+#pragma unroll
+      for (int k = 0; k < kSlicePanel; k++) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) a += q[k][e] * x[u][e];
+        a = wave_sum(a);
+        if (lane == 0) red[w][u * kSlicePanel + k] = a;
+      }
+    __syncthreads();
+    if (t < nb * kSlicePanel) {
+      const int u = t / kSlicePanel, k = t % kSlicePanel;
+      pd[((size_t)k * C + c0 + u) * nsl + b] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    }
+    __syncthreads();
+  }
+}
+
+// Totals of the panel's raw dots over the slices (slice_total's fixed
+// order): one wave per (panel vector k, later vector c); blockIdx.y picks
+// the matrix.
+__global__ __launch_bounds__(256) void mgs_slice_reduce_kernel(const MuonMat* __restrict__ mats, int nmat, int j0) {
+  const MuonMat& M = mats[blockIdx.y];
+  if (M.R <= kMaxPanelR) return;
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int k = p / C, c = p % C;
+  if (j1 >= C || k >= kSlicePanel || c < j1) return;
+  const float v = slice_total(slice_dots(M) + ((size_t)k * C + c) * nsl, nsl);
+  if ((threadIdx.x & 63) == 0) slice_dot_totals(M)[(size_t)k * C + c] = v;
+  (void)nmat;
+}
+
+// The panel's projections applied to every later vector, v_c -= sum_k d_kc
+// q_k (k ascending; every d_kc from the vector before this panel, as block
+// Gram-Schmidt takes them), and the column partials of the next panel's
+// first step (v_j1 . v_c for the next panel's vectors) into buffer j1 & 1.
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_update_kernel(const MuonMat* __restrict__ mats, int nmat,
+                                                                         int j0) {
+  static_assert(kSliceBatch == kSlicePanel, "the first batch is the next panel");
+  __shared__ float red[4][kSliceBatch];
+  int mi, b;
+  if (!slice_of(mats, nmat, mi, b)) return;
+  const MuonMat& M = mats[mi];
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
+  if (j1 >= C) return;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const SliceIO io(M, b);
+  const float* __restrict__ dd = slice_dot_totals(M);
+  float* __restrict__ Pout = M.red + (size_t)(j1 & 1) * C * nsl;
+  float q[kSlicePanel][kSliceEPT];
+#pragma unroll
+  for (int k = 0; k < kSlicePanel; k++) io.load(j0 + k, q[k]);
+  for (int c0 = j1; c0 < C; c0 += kSliceBatch) {
+    const int nb = min(kSliceBatch, C - c0);
+    float x[kSliceBatch][kSliceEPT];
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; u++) {
+      if (u < nb) {
+        io.load(c0 + u, x[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) x[u][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; u++) {
+      if (u >= nb) break;
+#pragma unroll
+      for (int k = 0; k < kSlicePanel; k++) {
+        const float d = dd[(size_t)k * C + c0 + u];
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) x[u][e] -= d * q[k][e];
+      }
+      io.store(c0 + u, x[u]);
+    }
+    if (c0 != j1) continue;
+    // the next panel's first column partials: v_j1 . v_c, j1 <= c < j1 + kSlicePanel
+#pragma unroll
+    for (int u = 0; u < kSliceBatch; u++) {
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < kSliceEPT; e++) a += x[0][e] * x[u][e];
+      a = wave_sum(a);
+      if (lane == 0) red[w][u] = a;
     }
     __syncthreads();
     if (t < nb) Pout[(size_t)(c0 + t) * nsl + b] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
@@ -669,7 +827,8 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
 }
 
 size_t mgs_red_floats(int64_t R, int64_t C) {
-  return R > kMaxPanelR ? (size_t)(2 * C * (int64_t)mgs_slices(R)) : 0;
+  // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl] and their totals [kSlicePanel][C]
+  return R > kMaxPanelR ? (size_t)((2 + kSlicePanel) * C * (int64_t)mgs_slices(R) + kSlicePanel * C) : 0;
 }
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
@@ -698,8 +857,27 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
       max_c = std::max(max_c, M.C);
     }
   }
-  for (int j = -1; slices > 0 && j < max_c_long; j++) {
-    hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j);
+  // Sliced path, in panels of kSlicePanel columns: MGS inside the panel (one
+  // launch per column, touching only the panel's vectors), then the
+  // panel's raw dots with every later vector, their totals, and the
+  // projections of every later vector (which also start the next panel).
+  if (slices > 0) {
+    hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, -1, kSlicePanel);
+    NSH_LAUNCHED();
+  }
+  for (int j0 = 0; slices > 0 && j0 < max_c_long; j0 += kSlicePanel) {
+    const int j1 = j0 + kSlicePanel;
+    for (int j = j0; j < j1 && j < max_c_long; j++) {
+      hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j, j1);
+      NSH_LAUNCHED();
+    }
+    if (j1 >= max_c_long) break;
+    hipLaunchKernelGGL(mgs_slice_dots_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j0);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(mgs_slice_reduce_kernel, dim3((unsigned)ceil_div(kSlicePanel * max_c_long, 4), nmat),
+                       dim3(256), 0, s, d_mats, nmat, j0);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(mgs_slice_update_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j0);
     NSH_LAUNCHED();
   }
   for (int jp = -kPB; jp + kPB < max_c; jp += kPB) {

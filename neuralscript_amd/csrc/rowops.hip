@@ -624,7 +624,7 @@ constexpr int kEmbRowsPerWg = 16;  // 16 waves of 64 lanes
 // LDS budget of the bitmaps: kEmbRowsPerWg * ceil(n/32) words.
 constexpr int64_t kEmbFusedMaxTokens = 32768;
 
-template <bool VEC, int NV, int kEmbAhead>
+template <bool VEC, int NV, int kEmbAhead, bool VEC_IDX>
 __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __restrict__ dout,
                                                               const float* __restrict__ idx,
                                                               float* __restrict__ dW, int64_t n, int64_t V,
@@ -635,20 +635,44 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
   const int64_t r0 = (int64_t)blockIdx.x * kEmbRowsPerWg;
   for (int i = t; i < kEmbRowsPerWg * nw; i += 1024) emb_bits[i] = 0u;
   __syncthreads();
-  // ids in batches of 8 per thread, all 8 loads issued before any is used
-  for (int64_t base = 0; base < n; base += 8 * 1024) {
-    float f[8];
+  // A token is this workgroup's when emb_row(id) lies in [r0, r0 + rows):
+  // tested in float, exactly (the bounds are integers below 2^24), as
+  // id >= r0 (id > -1 for r0 = 0: ids in (-1, 0) truncate to row 0) and
+  // id < min(r0 + rows, V); NaN fails both.  The row is then the truncation.
+  const bool first = r0 == 0;
+  const float lo = first ? -1.0f : (float)r0;
+  const float hi = (float)(r0 + kEmbRowsPerWg < V ? r0 + kEmbRowsPerWg : V);
+  auto mark = [&](float f, int64_t i) {
+    if ((first ? f > lo : f >= lo) && f < hi)
+      atomicOr(&emb_bits[((int)f - (int)r0) * nw + (int)(i >> 5)], 1u << (i & 31));
+  };
+  if (VEC_IDX) {  // float4 of ids, 4 per thread in flight, then the n % 4 tail
+    const float4* __restrict__ idx4 = reinterpret_cast<const float4*>(idx);
+    const int64_t n4 = n >> 2;
+    for (int64_t base = 0; base < n4; base += 4 * 1024) {
+      float4 f[4];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int64_t i = base + k * 1024 + t;
-      f[k] = i < n ? idx[i] : -1.0f;
+      for (int k = 0; k < 4; k++) {
+        const int64_t j = base + k * 1024 + t;
+        f[k] = j < n4 ? idx4[j] : make_float4(-1.f, -1.f, -1.f, -1.f);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int64_t i = 4 * (base + k * 1024 + t);
+        mark(f[k].x, i); mark(f[k].y, i + 1); mark(f[k].z, i + 2); mark(f[k].w, i + 3);
+      }
     }
+    if (t < (int)(n & 3)) mark(idx[4 * n4 + t], 4 * n4 + t);
+  } else {  // batches of 8 per thread, all 8 loads issued before any is used
+    for (int64_t base = 0; base < n; base += 8 * 1024) {
+      float f[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int64_t i = base + k * 1024 + t;
-      const int64_t lr = emb_row(f[k], V) - r0;  // out of range (and i >= n): -1 - r0 < 0
-      if (lr >= 0 && lr < kEmbRowsPerWg)
-        atomicOr(&emb_bits[(int)lr * nw + (int)(i >> 5)], 1u << (i & 31));
+      for (int k = 0; k < 8; k++) {
+        const int64_t i = base + k * 1024 + t;
+        f[k] = i < n ? idx[i] : -1.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; k++) mark(f[k], base + k * 1024 + t);
     }
   }
   __syncthreads();
@@ -742,13 +766,14 @@ __global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p
 // Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
 size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
 
-// One launch without workspace when the bitmaps fit in 64 KB of LDS and
-// the workgroups' shared reads of the ids stay small (n ids per workgroup).
+// One launch without workspace when the bitmaps fit in 64 KB of LDS, the
+// workgroups' shared reads of the ids stay small (n ids per workgroup) and
+// row numbers are exact in float (V <= 2^24).
 static bool emb_grad_fused_fits(int64_t n, int64_t V) {
-  return n <= kEmbFusedMaxTokens && n * ceil_div(V, kEmbRowsPerWg) <= ((int64_t)1 << 26);
+  return n <= kEmbFusedMaxTokens && V <= ((int64_t)1 << 24) && n * ceil_div(V, kEmbRowsPerWg) <= ((int64_t)1 << 26);
 }
 
-template <bool VEC>
+template <bool VEC, bool VEC_IDX>
 static void launch_emb_grad_fused(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                                   hipStream_t s) {
   const dim3 g((unsigned)ceil_div(V, kEmbRowsPerWg));
@@ -756,11 +781,20 @@ static void launch_emb_grad_fused(const float* dout, const float* idx, float* dW
   const int64_t DW = VEC ? D / 4 : D;
   // NV columns per lane per pass, AH rows in flight: NV * AH float4 of loads
   if (DW > 128)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
   else if (DW > 64)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
   else
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+}
+
+template <bool VEC>
+static void launch_emb_grad_fused_ids(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                                      hipStream_t s) {
+  if ((uintptr_t)idx % 16 == 0)
+    launch_emb_grad_fused<VEC, true>(dout, idx, dW, n, V, D, s);
+  else
+    launch_emb_grad_fused<VEC, false>(dout, idx, dW, n, V, D, s);
 }
 
 int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D, int* ws,
@@ -768,9 +802,9 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
   if (V <= 0 || D <= 0) return 0;  // dW is empty
   if (emb_grad_fused_fits(n, V)) {
     if (D % 4 == 0 && ((uintptr_t)dout | (uintptr_t)dW) % 16 == 0)
-      launch_emb_grad_fused<true>(dout, idx, dW, n, V, D, s);
+      launch_emb_grad_fused_ids<true>(dout, idx, dW, n, V, D, s);
     else
-      launch_emb_grad_fused<false>(dout, idx, dW, n, V, D, s);
+      launch_emb_grad_fused_ids<false>(dout, idx, dW, n, V, D, s);
     NSH_LAUNCHED();
     return 0;
   }

@@ -21,13 +21,15 @@ def ws(r, c):
 # length class, 1 (<= 512), 2 (<= 1024), 4, 8 (<= 4096) and 16 (<= 8192)
 # elements a thread, with float4 rows (length % 4 == 0) and scalar ones, and
 # ragged last panels (vector counts not multiples of 8).
-# (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001): vectors
-# longer than 8192 floats take the sliced path (2048-float slices, one launch
-# per column) instead of the register panels; odd lengths take its scalar
-# loads, 19 vectors a ragged last batch of 3
+# (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001), (262144, 64),
+# (64, 100000): vectors longer than 8192 floats take the sliced path
+# (2048-float slices, panels of 8 columns: MGS inside a panel, block
+# projections across panels) instead of the register panels; odd lengths
+# take its scalar loads, 19 vectors a ragged last panel of 3
 @pytest.mark.parametrize("r,c", [(16, 16), (40, 16), (16, 24), (64, 24), (512, 512), (2048, 512), (512, 8192),
                                  (1000, 40), (3001, 24), (4096, 20), (5001, 24), (24, 6000), (8192, 9),
-                                 (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001)])
+                                 (9000, 24), (24, 9000), (8193, 40), (20000, 19), (19, 20001), (262144, 64),
+                                 (64, 100000)])
 def test_orthonormalize_matches_oracle_mgs(r, c):
     """Q within the fp32 bar (1e-5 + 1e-4 |ref|) of the oracle's.  A square
     Gaussian matrix is ill-conditioned (cond ~ n), and MGS's Q moves by ~eps
@@ -114,3 +116,25 @@ def test_muon_multi_matches_oracle(shapes):
         ref = ws_[i].copy()
         oracle.lib().or_muon_step(oracle.fp(ref), oracle.fp(gs_[i].copy()), r, c, ctypes.c_float(0.02))
         helpers.assert_close(dw[i].to_host(), ref, f"muon multi matrix {i} {r}x{c}")
+
+
+@pytest.mark.parametrize("r,c,zero", [(24, 9000, (3, 10, 17)), (20000, 19, (0, 8, 18))])
+def test_sliced_orthonormalize_with_zero_vectors(r, c, zero):
+    """Zero gradient vectors (a MoE expert without tokens) on the sliced
+    path: MGS's +1e-30 guard gives them q = 0, in the panel that holds them
+    and as projections of the later panels; everything else as the oracle."""
+    print(f"mgs zero vectors {r}x{c} {zero}", flush=True)
+    g = synth.normal(r * 5 + c, r * c).reshape(r, c)
+    for z in zero:
+        if r < c:
+            g[z, :] = 0.0
+        else:
+            g[:, z] = 0.0
+    g = g.ravel()
+    q = DA(r * c)
+    runtime.op("orthonormalize", DA.from_host(g), q, r, c, ws(r, c))
+    got = q.to_host()
+    helpers.assert_close(got, oracle.orthonom(g, r, c), f"mgs {r}x{c} with zero vectors")
+    Q = got.reshape(r, c)
+    for z in zero:
+        assert not np.any(Q[z, :] if r < c else Q[:, z]), z
