@@ -115,7 +115,17 @@ struct MuonMat {
 size_t mgs_red_floats(int64_t R, int64_t C);
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 // MGS of every matrix: T holds the vectors on entry, the q vectors on exit.
-int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s);
+// Longest vector the register-panel MGS takes; longer ones go through the
+// sliced path (and need MuonMat::red).
+int64_t mgs_max_panel_len();
+// A second stream for the sliced-path launches of launch_mgs, and the two
+// events (no timing) that fork it from and join it back to the main stream.
+struct MgsSide {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s,
+               const MgsSide* side = nullptr);
 int launch_muon_update(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s);
 
 // peak.hip -----------------------------------------------------------------------

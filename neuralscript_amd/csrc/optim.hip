@@ -826,6 +826,8 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
   return 0;
 }
 
+int64_t mgs_max_panel_len() { return kMaxPanelR; }
+
 size_t mgs_red_floats(int64_t R, int64_t C) {
   // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl] and their totals [kSlicePanel][C]
   return R > kMaxPanelR ? (size_t)((2 + kSlicePanel) * C * (int64_t)mgs_slices(R) + kSlicePanel * C) : 0;
@@ -840,7 +842,7 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
   return 0;
 }
 
-int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s) {
+int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream_t s, const MgsSide* side) {
   if (nmat <= 0) return 0;
   // panel path for vectors up to kMaxPanelR long, sliced path beyond
   int max_c = 0, max_c_long = 0, slices = 0;
@@ -857,29 +859,40 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
       max_c = std::max(max_c, M.C);
     }
   }
+  // The two paths touch disjoint matrices.  With both present and a side
+  // stream given, the sliced launches (bound by HBM) run on the side stream
+  // beside the panel launches (bound by one workgroup's chain), forked from
+  // and joined back to s by events.
+  const bool fork = side && side->stream && slices > 0 && max_c > 0;
+  hipStream_t ss = fork ? side->stream : s;
+  if (fork) {
+    NSH_CHECK(hipEventRecord(side->fork, s));
+    NSH_CHECK(hipStreamWaitEvent(ss, side->fork, 0));
+  }
   // Sliced path, in panels of kSlicePanel columns: MGS inside the panel (one
   // launch per column, touching only the panel's vectors), then the
   // panel's raw dots with every later vector, their totals, and the
   // projections of every later vector (which also start the next panel).
   if (slices > 0) {
-    hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, -1, kSlicePanel);
+    hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, -1, kSlicePanel);
     NSH_LAUNCHED();
   }
   for (int j0 = 0; slices > 0 && j0 < max_c_long; j0 += kSlicePanel) {
     const int j1 = j0 + kSlicePanel;
     for (int j = j0; j < j1 && j < max_c_long; j++) {
-      hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j, j1);
+      hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, j, j1);
       NSH_LAUNCHED();
     }
     if (j1 >= max_c_long) break;
-    hipLaunchKernelGGL(mgs_slice_dots_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j0);
+    hipLaunchKernelGGL(mgs_slice_dots_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, j0);
     NSH_LAUNCHED();
     hipLaunchKernelGGL(mgs_slice_reduce_kernel, dim3((unsigned)ceil_div(kSlicePanel * max_c_long, 4), nmat),
-                       dim3(256), 0, s, d_mats, nmat, j0);
+                       dim3(256), 0, ss, d_mats, nmat, j0);
     NSH_LAUNCHED();
-    hipLaunchKernelGGL(mgs_slice_update_kernel, dim3(slices), dim3(kSliceThreads), 0, s, d_mats, nmat, j0);
+    hipLaunchKernelGGL(mgs_slice_update_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, j0);
     NSH_LAUNCHED();
   }
+  if (fork) NSH_CHECK(hipEventRecord(side->join, ss));
   for (int jp = -kPB; jp + kPB < max_c; jp += kPB) {
     int grid = 0;
     for (int i = 0; i < nmat; i++) {
@@ -889,6 +902,7 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
     hipLaunchKernelGGL(mgs_panel_kernel, dim3(grid), dim3(kPanelThreads), 0, s, d_mats, nmat, jp);
     NSH_LAUNCHED();
   }
+  if (fork) NSH_CHECK(hipStreamWaitEvent(s, side->join, 0));
   return 0;
 }
 

@@ -612,28 +612,32 @@ __global__ __launch_bounds__(256) void emb_grad_rows_vec_kernel(const float* __r
 }
 
 // ---- embedding weight gradient in one launch (no sort, no workspace) --------
-// Each workgroup owns kEmbRowsPerWg consecutive vocabulary rows.  It reads
-// every token id once (the ids are shared by all workgroups, so they come
-// from L2) and marks the tokens that hit its rows in one LDS bitmap per row,
-// bit t = token t.  Walking a row's bitmap word by word and bit by bit
-// visits its tokens in ascending order, so each output element is the
-// reference's sequential sum with no sort at all.  One wave per row: it
-// gathers the row's tokens' gradient rows (kEmbAhead loads in flight) and
-// adds them in token order, then writes the dW row once (zeros if no token).
-constexpr int kEmbRowsPerWg = 16;  // 16 waves of 64 lanes
-// LDS budget of the bitmaps: kEmbRowsPerWg * ceil(n/32) words.
+// Each workgroup owns 16 * RPW consecutive vocabulary rows.  It reads every
+// token id once (the ids are shared by all workgroups, so they come from L2)
+// and marks the tokens that hit its rows in one LDS bitmap per row, bit t =
+// token t.  Walking a row's bitmap word by word and bit by bit visits its
+// tokens in ascending order, so each output element is the reference's
+// sequential sum with no sort at all.  Each wave owns RPW rows (rows wv,
+// wv + 16, ...): it gathers a row's tokens' gradient rows (kEmbAhead loads in
+// flight) and adds them in token order, then writes the dW row once (zeros if
+// no token).  Two rows per wave halve the workgroups that each scan all ids
+// (c5's 16384 ids over 8192 rows: 18.3 -> 15.2 us); they are used when the
+// grid still holds a workgroup per CU.
+constexpr int kEmbWaves = 16;  // 16 waves of 64 lanes
+// LDS budget of the bitmaps: 16 * RPW * ceil(n/32) words (128 KB at RPW 2).
 constexpr int64_t kEmbFusedMaxTokens = 32768;
 
-template <bool VEC, int NV, int kEmbAhead, bool VEC_IDX>
+template <bool VEC, int NV, int kEmbAhead, bool VEC_IDX, int RPW>
 __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __restrict__ dout,
                                                               const float* __restrict__ idx,
                                                               float* __restrict__ dW, int64_t n, int64_t V,
                                                               int64_t D) {
+  constexpr int kRows = kEmbWaves * RPW;
   extern __shared__ unsigned emb_bits[];
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int nw = (int)((n + 31) >> 5);
-  const int64_t r0 = (int64_t)blockIdx.x * kEmbRowsPerWg;
-  for (int i = t; i < kEmbRowsPerWg * nw; i += 1024) emb_bits[i] = 0u;
+  const int64_t r0 = (int64_t)blockIdx.x * kRows;
+  for (int i = t; i < kRows * nw; i += 1024) emb_bits[i] = 0u;
   __syncthreads();
   // A token is this workgroup's when emb_row(id) lies in [r0, r0 + rows):
   // tested in float, exactly (the bounds are integers below 2^24), as
@@ -641,7 +645,7 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
   // id < min(r0 + rows, V); NaN fails both.  The row is then the truncation.
   const bool first = r0 == 0;
   const float lo = first ? -1.0f : (float)r0;
-  const float hi = (float)(r0 + kEmbRowsPerWg < V ? r0 + kEmbRowsPerWg : V);
+  const float hi = (float)(r0 + kRows < V ? r0 + kRows : V);
   auto mark = [&](float f, int64_t i) {
     if ((first ? f > lo : f >= lo) && f < hi)
       atomicOr(&emb_bits[((int)f - (int)r0) * nw + (int)(i >> 5)], 1u << (i & 31));
@@ -676,82 +680,84 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
     }
   }
   __syncthreads();
-  const int64_t r = r0 + wv;
-  if (r >= V) return;
-  const unsigned* __restrict__ bits = emb_bits + wv * nw;
   // Columns per pass: 64 lanes x NV float4 (VEC) or 64 lanes x NV floats.
   constexpr int W = VEC ? 4 : 1;
   const int64_t DW = D / W;
-  // The pass loop is wave-uniform (every lane takes part in the ballots and
-  // lane reads below); lanes past the row's end only skip their loads/stores.
-  for (int64_t cb = 0; cb < DW; cb += 64 * NV) {
-    const int64_t c0 = cb + lane;
-    float acc[NV][W];
-    float buf[kEmbAhead][NV][W];
+  for (int rr = 0; rr < RPW; rr++) {
+    const int64_t r = r0 + wv + kEmbWaves * rr;
+    if (r >= V) return;
+    const unsigned* __restrict__ bits = emb_bits + (wv + kEmbWaves * rr) * nw;
+    // The pass loop is wave-uniform (every lane takes part in the ballots and
+    // lane reads below); lanes past the row's end only skip their loads/stores.
+    for (int64_t cb = 0; cb < DW; cb += 64 * NV) {
+      const int64_t c0 = cb + lane;
+      float acc[NV][W];
+      float buf[kEmbAhead][NV][W];
 #pragma unroll
-    for (int j = 0; j < NV; j++)
+      for (int j = 0; j < NV; j++)
 #pragma unroll
-      for (int k = 0; k < W; k++) acc[j][k] = 0.f;
-    int pend = 0;  // loads in flight, oldest in slot (head % kEmbAhead)
-    int head = 0;
-    auto add_oldest = [&]() {
-      const int s = head % kEmbAhead;
+        for (int k = 0; k < W; k++) acc[j][k] = 0.f;
+      int pend = 0;  // loads in flight, oldest in slot (head % kEmbAhead)
+      int head = 0;
+      auto add_oldest = [&]() {
+        const int s = head % kEmbAhead;
 #pragma unroll
-      for (int q = 0; q < kEmbAhead; q++)
-        if (q == s)
+        for (int q = 0; q < kEmbAhead; q++)
+          if (q == s)
 #pragma unroll
-          for (int j = 0; j < NV; j++)
+            for (int j = 0; j < NV; j++)
 #pragma unroll
-            for (int k = 0; k < W; k++) acc[j][k] += buf[q][j][k];
-      head++;
-      pend--;
-    };
-    for (int w0 = 0; w0 < nw; w0 += 64) {
-      const unsigned word = w0 + lane < nw ? bits[w0 + lane] : 0u;
-      uint64_t nz = __ballot(word != 0u);
-      while (nz) {
-        const int l = __builtin_ctzll(nz);
-        nz &= nz - 1;
-        unsigned wd = (unsigned)__builtin_amdgcn_readlane((int)word, l);
-        while (wd) {
-          const int b = __builtin_ctz(wd);
-          wd &= wd - 1;
-          const int64_t tok = (int64_t)(w0 + l) * 32 + b;
-          if (pend == kEmbAhead) add_oldest();
-          const int s = (head + pend) % kEmbAhead;
-          const float* src = dout + tok * D;
+              for (int k = 0; k < W; k++) acc[j][k] += buf[q][j][k];
+        head++;
+        pend--;
+      };
+      for (int w0 = 0; w0 < nw; w0 += 64) {
+        const unsigned word = w0 + lane < nw ? bits[w0 + lane] : 0u;
+        uint64_t nz = __ballot(word != 0u);
+        while (nz) {
+          const int l = __builtin_ctzll(nz);
+          nz &= nz - 1;
+          unsigned wd = (unsigned)__builtin_amdgcn_readlane((int)word, l);
+          while (wd) {
+            const int b = __builtin_ctz(wd);
+            wd &= wd - 1;
+            const int64_t tok = (int64_t)(w0 + l) * 32 + b;
+            if (pend == kEmbAhead) add_oldest();
+            const int s = (head + pend) % kEmbAhead;
+            const float* src = dout + tok * D;
 #pragma unroll
-          for (int q = 0; q < kEmbAhead; q++)
-            if (q == s)
+            for (int q = 0; q < kEmbAhead; q++)
+              if (q == s)
 #pragma unroll
-              for (int j = 0; j < NV; j++) {
-                const int64_t c = c0 + 64 * j;
-                if (c < DW) {
-                  if constexpr (VEC) {
-                    const float4 v = reinterpret_cast<const float4*>(src)[c];
-                    buf[q][j][0] = v.x; buf[q][j][1] = v.y; buf[q][j][2] = v.z; buf[q][j][3] = v.w;
+                for (int j = 0; j < NV; j++) {
+                  const int64_t c = c0 + 64 * j;
+                  if (c < DW) {
+                    if constexpr (VEC) {
+                      const float4 v = reinterpret_cast<const float4*>(src)[c];
+                      buf[q][j][0] = v.x; buf[q][j][1] = v.y; buf[q][j][2] = v.z; buf[q][j][3] = v.w;
+                    } else {
+                      buf[q][j][0] = src[c];
+                    }
                   } else {
-                    buf[q][j][0] = src[c];
-                  }
-                } else {
 #pragma unroll
-                  for (int k = 0; k < W; k++) buf[q][j][k] = 0.f;
+                    for (int k = 0; k < W; k++) buf[q][j][k] = 0.f;
+                  }
                 }
-              }
-          pend++;
+            pend++;
+          }
         }
       }
-    }
-    while (pend > 0) add_oldest();
-    float* o = dW + r * D;
+      while (pend > 0) add_oldest();
+      float* o = dW + r * D;
 #pragma unroll
-    for (int j = 0; j < NV; j++) {
-      const int64_t c = c0 + 64 * j;
-      if (c < DW) {
-        if constexpr (VEC)
-          reinterpret_cast<float4*>(o)[c] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
-        else
-          o[c] = acc[j][0];
+      for (int j = 0; j < NV; j++) {
+        const int64_t c = c0 + 64 * j;
+        if (c < DW) {
+          if constexpr (VEC)
+            reinterpret_cast<float4*>(o)[c] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+          else
+            o[c] = acc[j][0];
+        }
       }
     }
   }
@@ -766,26 +772,39 @@ __global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p
 // Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
 size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
 
-// One launch without workspace when the bitmaps fit in 64 KB of LDS, the
+// One launch without workspace when the bitmaps fit in LDS, the
 // workgroups' shared reads of the ids stay small (n ids per workgroup) and
 // row numbers are exact in float (V <= 2^24).
 static bool emb_grad_fused_fits(int64_t n, int64_t V) {
-  return n <= kEmbFusedMaxTokens && V <= ((int64_t)1 << 24) && n * ceil_div(V, kEmbRowsPerWg) <= ((int64_t)1 << 26);
+  return n <= kEmbFusedMaxTokens && V <= ((int64_t)1 << 24) && n * ceil_div(V, kEmbWaves) <= ((int64_t)1 << 26);
+}
+
+// Rows per wave: 2 while that still leaves a workgroup for each of the 256
+// CUs, else 1.
+static int emb_grad_rows_per_wave(int64_t V) { return ceil_div(V, 2 * kEmbWaves) >= 256 ? 2 : 1; }
+
+template <bool VEC, bool VEC_IDX, int RPW>
+static void launch_emb_grad_fused_rpw(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
+                                      hipStream_t s) {
+  const dim3 g((unsigned)ceil_div(V, kEmbWaves * RPW));
+  const size_t lds = (size_t)kEmbWaves * RPW * (size_t)((n + 31) >> 5) * sizeof(unsigned);
+  const int64_t DW = VEC ? D / 4 : D;
+  // NV columns per lane per pass, AH rows in flight: NV * AH float4 of loads
+  if (DW > 128)
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+  else if (DW > 64)
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+  else
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
 }
 
 template <bool VEC, bool VEC_IDX>
 static void launch_emb_grad_fused(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                                   hipStream_t s) {
-  const dim3 g((unsigned)ceil_div(V, kEmbRowsPerWg));
-  const size_t lds = (size_t)kEmbRowsPerWg * (size_t)((n + 31) >> 5) * sizeof(unsigned);
-  const int64_t DW = VEC ? D / 4 : D;
-  // NV columns per lane per pass, AH rows in flight: NV * AH float4 of loads
-  if (DW > 128)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
-  else if (DW > 64)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+  if (emb_grad_rows_per_wave(V) == 2)
+    launch_emb_grad_fused_rpw<VEC, VEC_IDX, 2>(dout, idx, dW, n, V, D, s);
   else
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4, VEC_IDX>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    launch_emb_grad_fused_rpw<VEC, VEC_IDX, 1>(dout, idx, dW, n, V, D, s);
 }
 
 template <bool VEC>

@@ -89,6 +89,9 @@ struct ns_model {
   hipStream_t copy_stream = nullptr;
   hipEvent_t labels_ev = nullptr;
   hipEvent_t before_ev = nullptr;   // the model's stream before this call's kernels
+  // Muon's sliced-path stream (created when a step has both long and short
+  // Muon matrices), forked from and joined back to `stream` inside a step
+  nship::MgsSide muon_side;
   // profiling
   bool prof = false;
   std::vector<ProfEntry> pending;
@@ -733,9 +736,16 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
     Prof p(m, "muon_gather");
     if (launch_muon_gather(d, nm, max_elems, s) != 0) return -1;
   }
+  bool long_vec = false, short_vec = false;
+  for (const MuonMat& mm : m->muon_host) (mm.R > mgs_max_panel_len() ? long_vec : short_vec) = true;
+  if (long_vec && short_vec && !m->muon_side.stream) {
+    NSH_CHECK(hipEventCreateWithFlags(&m->muon_side.fork, hipEventDisableTiming));
+    NSH_CHECK(hipEventCreateWithFlags(&m->muon_side.join, hipEventDisableTiming));
+    NSH_CHECK(hipStreamCreateWithFlags(&m->muon_side.stream, hipStreamNonBlocking));
+  }
   {
     Prof p(m, "muon_mgs");
-    if (launch_mgs(d, m->muon_host.data(), nm, s) != 0) return -1;
+    if (launch_mgs(d, m->muon_host.data(), nm, s, &m->muon_side) != 0) return -1;
   }
   Prof p(m, "muon_update");
   return launch_muon_update(d, nm, max_elems, s);
@@ -1210,6 +1220,12 @@ void nsh_model_free(ns_model* m) {
   if (m->labels_ev) hipEventDestroy(m->labels_ev);
   if (m->before_ev) hipEventDestroy(m->before_ev);
   if (m->copy_stream) hipStreamDestroy(m->copy_stream);
+  if (m->muon_side.stream) {
+    hipStreamSynchronize(m->muon_side.stream);
+    hipStreamDestroy(m->muon_side.stream);
+  }
+  if (m->muon_side.fork) hipEventDestroy(m->muon_side.fork);
+  if (m->muon_side.join) hipEventDestroy(m->muon_side.join);
   for (auto& b : m->arena) if (b.p) hipFree(b.p);
   for (auto& kv : m->scratch) if (kv.second.p) hipFree(kv.second.p);
   for (auto& kv : m->dev_idx) if (kv.second) hipFree(kv.second);
