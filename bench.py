@@ -187,12 +187,18 @@ def _setup(key):
     return runtime, workloads, wl, plan, w
 
 
-def _timed(model, step, steps, warmup):
-    """warmup untimed calls, then `steps` timed calls with per-launch HIP
-    events on the model's stream; synchronised on both sides."""
+def _timed(model, step, steps, warmup, timed_regions):
+    """warmup untimed calls, then `steps` timed calls synchronised on both
+    sides, in which HIP events on the model's stream bracket only the
+    launches of `timed_regions` (the roofline's: every event pair leaves a
+    gap of a few microseconds between launches, ~0.24 ms per c5 step if every
+    region were timed); then `steps` more calls with every region timed, for
+    the per-region breakdown.  The timed regions' figures in the returned
+    profile are the timed run's."""
     for _ in range(warmup):
         step()
     model.sync()
+    model.profile_select(timed_regions)
     model.profile(True)
     model.profile_reset()
     t0 = time.perf_counter()
@@ -200,10 +206,27 @@ def _timed(model, step, steps, warmup):
         step()
     model.sync()
     dt = time.perf_counter() - t0
+    timed = model.profile_report()
+    model.profile_select(None)
+    model.profile_reset()
+    for _ in range(steps):
+        step()
+    model.sync()
     prof = model.profile_report()
     model.profile(False)
+    prof.update(timed)
     prof["_steps"] = steps
     return dt, prof
+
+
+KERNELS_NOTE = ("per profile region, HIP events around each launch, from a second run of the same number of "
+                "steps after the timed one; the roofline region's figures are the timed run's")
+
+
+def _roof_regions(key):
+    """Profile regions of config `key`'s dominant kernel (and its variants)."""
+    region = DOMINANT[key][0]
+    return list(REGION_VARIANTS.get(region, (region,)))
 
 
 def bench_forward(key, steps, warmup, with_cpu, budget):
@@ -213,7 +236,7 @@ def bench_forward(key, steps, warmup, with_cpu, budget):
     model = runtime.Model(plan, w)
     dx = runtime.DeviceArray.from_host(x)
     dy = runtime.DeviceArray(wl.rows * plan.out_cols)
-    dt, prof = _timed(model, lambda: model.eval_infer_device(dx, dy), steps, warmup)
+    dt, prof = _timed(model, lambda: model.eval_infer_device(dx, dy), steps, warmup, _roof_regions(key))
     out = dy.to_host()
     if not np.isfinite(out).all():
         raise SystemExit(f"bench.py: non-finite {key} output")
@@ -236,7 +259,7 @@ def bench_forward(key, steps, warmup, with_cpu, budget):
     hbm = {k: v for k, v in work.items() if k in HBM_REGIONS}
     res = {"value": wl.rows * steps / dt, "unit": "tokens/s", "ms_per_step": dt * 1e3 / steps,
            "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_eval_infer_device",
-           "roofline": roofline_of(key, work, prof), "kernels": kernel_table(prof, steps, work, hbm),
+           "roofline": roofline_of(key, work, prof), "kernels_note": KERNELS_NOTE, "kernels": kernel_table(prof, steps, work, hbm),
            "host_abi": {"tokens_per_s": wl.rows / abi_dt, "ms": abi_dt * 1e3,
                         "note": "ns_eval_infer with host buffers (PCIe-inclusive)"}}
     if routing is not None:
@@ -313,7 +336,7 @@ def bench_train(key, steps, warmup, with_cpu, budget):
         model.train_step_device(dx, dy, 3e-4 * min(1.0, t[0] / 100.0), want_loss=False)
         t[0] += 1
 
-    dt, prof = _timed(model, step, steps, warmup)
+    dt, prof = _timed(model, step, steps, warmup, _roof_regions(key))
     loss = model.train_step_device(dx, dy, 3e-4 * min(1.0, t[0] / 100.0))
     t[0] += 1
     # host-pointer ABI (ns_runtime_train_step: the [M, C] one-hot labels cross
@@ -335,7 +358,8 @@ def bench_train(key, steps, warmup, with_cpu, budget):
     res = {"value": steps / dt, "unit": "steps/s", "ms_per_step": dt * 1e3 / steps,
            "workload": f"{key}: {wl.desc}", "tokens": wl.rows, "entry": "nsh_train_step_device",
            "achieved_TFLOP/s": work["total"] / (dt / steps) / 1e12, "last_loss": float(loss),
-           "roofline": roofline_of(key, work, prof), "kernels": kernel_table(prof, steps, work, c5_hbm_bytes(n_muon)),
+           "roofline": roofline_of(key, work, prof), "kernels_note": KERNELS_NOTE,
+           "kernels": kernel_table(prof, steps, work, c5_hbm_bytes(n_muon)),
            "adamw": adamw_bandwidth(n_muon), "row_kernels": row_kernels,
            "host_abi": {"steps_per_s": 1.0 / abi_dt, "ms": abi_dt * 1e3,
                         "note": "ns_runtime_train_step with host buffers (labels uploaded every call)"}}
@@ -357,14 +381,15 @@ def bench_moe_backward(steps, warmup):
     w, x, y = workloads.moe_training_workload(M)
     model = runtime.Model(plan, w)
     dx, dy = runtime.DeviceArray.from_host(x), runtime.DeviceArray.from_host(y)
-    dt, prof = _timed(model, lambda: model.train_step_device(dx, dy, 0.0, want_loss=False), steps, warmup)
+    dt, prof = _timed(model, lambda: model.train_step_device(dx, dy, 0.0, want_loss=False), steps, warmup,
+                      ["moe_bwd_grouped", "moe_bwd_kgrouped"])
     model.free()
     dx.free()
     dy.free()
     work = {"moe_bwd_grouped": 4.0 * M * D * H, "moe_bwd_kgrouped": 4.0 * M * D * H}
     out = {"workload": "MoE backward at config 4's expert shape: moep (emb 8192x1024 -> MoE D 1024, E 64, "
                        "FFN 1024 -> fc 16), 4096 Zipf-routed tokens, train step at lr 0",
-           "kernels": kernel_table(prof, steps, work, {})}
+           "kernels_note": KERNELS_NOTE, "kernels": kernel_table(prof, steps, work, {})}
     for region, flop in work.items():
         ms = prof[region]["ms"] / prof[region]["calls"]
         tf = flop / (ms * 1e-3) / 1e12

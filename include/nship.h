@@ -131,6 +131,11 @@ int nsh_model_last_routing(ns_model* m, int32_t* best, float* prob, float* logit
 /* Per-kernel timing with HIP events recorded on the model's stream around
  * every launch.  The report is one JSON object: kernel -> {calls, ms}. */
 int nsh_profile_enable(ns_model* m, int on);
+/* Limit the event pairs to the listed regions (comma-separated names, e.g.
+ * "attention_bwd,gemm"); NULL or "" times every region.  Each event pair
+ * leaves a gap of a few microseconds between launches, so a timed run that
+ * needs only one region's figure selects it. */
+int nsh_profile_select(ns_model* m, const char* regions);
 int nsh_profile_reset(ns_model* m);
 int nsh_profile_report(ns_model* m, char* buf, size_t len);
 

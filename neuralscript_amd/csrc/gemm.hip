@@ -90,10 +90,19 @@ struct Stage {
       }
     }
   }
+  // K-blocked operand (kblk_ > 0, VEC only): slab k0 lies in block k0 / kblk_
+  int kblk_ = 0;
+  int64_t sk_ = 0;
   template <bool CHK = true>
   __device__ __forceinline__ void load(int64_t ld, int k0, int K, int t) {
     if (VEC) {
-      const int64_t off = KC ? (int64_t)k0 : (int64_t)k0 * ld;
+      int64_t kb = 0;
+      int kl = k0;
+      if (kblk_) {
+        kb = (int64_t)(k0 / kblk_) * sk_;
+        kl = k0 % kblk_;
+      }
+      const int64_t off = kb + (KC ? (int64_t)kl : (int64_t)kl * ld);
 #pragma unroll
       for (int i = 0; i < kVec; i++) {
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -176,32 +185,83 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm
 }
 
 // Plain epilogue C = acc * act'(aux) for one wave's 64x64 block (aux with
-// C's row and column indices, pitch ldaux): each 32x32 block's 16 aux values
-// load together, then its stores.  Its own loop nest, so that the main
-// epilogue's loops stay fully unrolled and the accumulators in registers.
+// C's row and column indices, pitch ldaux): the four 32x32 blocks' aux
+// values are loaded one block ahead of that block's stores (the loads of
+// block b + 1 are in flight while block b is stored).  Its own loop nest, so
+// that the main epilogue's loops stay fully unrolled and the accumulators in
+// registers.
 template <int CODE>
 __device__ __forceinline__ void store_act_grad(const floatx16 (&acc)[2][2], const GemmArgs& g, float* __restrict__ C,
                                                int m0, int n0, int wm, int wn, int l32, int kh, int m_end) {
+  if (g.mask_in) {
+    // relu' from the sign bits: one 16-bit load per lane and 32x32 block,
+    // bit v for the lane's accumulator v (the layout the forward wrote)
+    unsigned bits[4];
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+      const int col = n0 + wn * 64 + (blk & 1) * 32 + l32;
+      const int rb = m0 + wm * 64 + (blk >> 1) * 32;
+      bits[blk] = col < g.N && rb < m_end ? g.mask_in[(int64_t)(2 * (rb / 32) + kh) * g.ldmask + col] : 0u;
+    }
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) {
+      const int r = blk >> 1, c = blk & 1;
+      const int col = n0 + wn * 64 + c * 32 + l32;
+      const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
+      const bool cin = col < g.N;
+      float* cp = C + (int64_t)row0 * g.ldc + col;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int dr = 8 * (v >> 2) + (v & 3);
+        if (cin && row0 + dr < m_end) cp[(int64_t)dr * g.ldc] = acc[r][c][v] * ((bits[blk] >> v) & 1u ? 1.f : 0.f);
+      }
+    }
+    return;
+  }
+  float au[2][16];
+  auto load = [&](int blk, float(&dst)[16]) {
+    const int col = n0 + wn * 64 + (blk & 1) * 32 + l32;
+    const int row0 = m0 + wm * 64 + (blk >> 1) * 32 + 4 * kh;
+    const bool cin = col < g.N;
+    const float* ap = g.aux + (int64_t)row0 * g.ldaux + col;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int dr = 8 * (v >> 2) + (v & 3);
+      dst[v] = cin && row0 + dr < m_end ? ap[(int64_t)dr * g.ldaux] : 0.f;
+    }
+  };
+  load(0, au[0]);
+#pragma unroll
+  for (int blk = 0; blk < 4; blk++) {
+    if (blk + 1 < 4) load(blk + 1, au[(blk + 1) & 1]);
+    const int r = blk >> 1, c = blk & 1;
+    const int col = n0 + wn * 64 + c * 32 + l32;
+    const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
+    const bool cin = col < g.N;
+    float* cp = C + (int64_t)row0 * g.ldc + col;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+      const int dr = 8 * (v >> 2) + (v & 3);
+      if (cin && row0 + dr < m_end) cp[(int64_t)dr * g.ldc] = acc[r][c][v] * act_deriv(au[blk & 1][v], CODE);
+    }
+  }
+}
+
+// Sign bits of the pre-activation for a relu gradient later (the layout of
+// GemmArgs::mask_out): each lane's 16 rows of a 32x32 block in one 16-bit
+// value.  Its own loop nest, as store_act_grad.
+__device__ __forceinline__ void store_relu_bits(const floatx16 (&acc)[2][2], const GemmArgs& g, int m0, int n0, int wm,
+                                                int wn, int l32, int kh, int m_end) {
 #pragma unroll
   for (int r = 0; r < 2; r++)
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const int col = n0 + wn * 64 + c * 32 + l32;
-      const int row0 = m0 + wm * 64 + r * 32 + 4 * kh;
-      const bool cin = col < g.N;
-      const float* ap = g.aux + (int64_t)row0 * g.ldaux + col;
-      float* cp = C + (int64_t)row0 * g.ldc + col;
-      float au[16];
+      const int rb = m0 + wm * 64 + r * 32;
+      unsigned bits = 0u;
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int dr = 8 * (v >> 2) + (v & 3);
-        au[v] = cin && row0 + dr < m_end ? ap[(int64_t)dr * g.ldaux] : 0.f;
-      }
-#pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int dr = 8 * (v >> 2) + (v & 3);
-        if (cin && row0 + dr < m_end) cp[(int64_t)dr * g.ldc] = acc[r][c][v] * act_deriv(au[v], CODE);
-      }
+      for (int v = 0; v < 16; v++) bits |= (acc[r][c][v] > 0.f ? 1u : 0u) << v;
+      if (col < g.N && rb < m_end) g.mask_out[(int64_t)(2 * (rb / 32) + kh) * g.ldmask + col] = (uint16_t)bits;
     }
 }
 
@@ -280,6 +340,10 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
   // (the 256-row tiles never gather rows)
   sa.init(A, lda, m0, m_end, t, WMW == 2 ? nullptr : g.a_rows);
   sb.init(B, ldb, n0, N, t);
+  sa.kblk_ = g.kblk;
+  sa.sk_ = g.sAk;
+  sb.kblk_ = g.kblk;
+  sb.sk_ = g.sBk;
   sa.load(lda, kbeg, kend, t);
   sb.load(ldb, kbeg, kend, t);
   sa.store(smem, t);
@@ -340,6 +404,7 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
       store_act_grad<kActRelu>(acc, g, C, m0, n0, wm, wn, l32, kh, m_end);
       return;
     }
+    if (g.mask_out) store_relu_bits(acc, g, m0, n0, wm, wn, l32, kh, m_end);
     // plain stores, the activation resolved once per 32x32 block
 #pragma unroll
     for (int r = 0; r < 2; r++)
@@ -434,9 +499,25 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // training MLPs'); the others take the general epilogue.
 static bool plain_act_grad(const GemmArgs& g) { return g.mode == kEpiActGrad && g.aux && g.act == kActRelu; }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t s) {
   if (in.M <= 0 || in.N <= 0 || batch <= 0) return 0;
   GemmArgs g = in;
+  if (g.kblk && (g.kblk % BK != 0 || g.kseg || g.groups)) {
+    set_error("gemm: K blocks must be a multiple of 16 and exclude K-grouped and grouped modes");
+    return -1;
+  }
   // float4 staging needs each operand's contiguous extent, leading dimension,
   // batch stride and base to be 4-float aligned.
   // (K-grouped segments start anywhere, so a k-contiguous operand needs the
@@ -445,7 +526,11 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
                   (tA || !g.kseg);
   const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
                   (!tB || !g.kseg);
-  const bool vec = va && vb;
+  const bool vec = va && vb && (!g.kblk || (g.sAk % 4 == 0 && g.sBk % 4 == 0));
+  if (g.kblk && !vec) {
+    set_error("gemm: K-blocked operands need 16-byte aligned, 4-float strided operands");
+    return -1;
+  }
   // plain epilogue: no row maps or scaling; activation, activation gradient,
   // accumulate or the pre-activation / activation pair (kchunk partials are
   // always kEpiAct)
@@ -453,6 +538,11 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
                      (g.mode == kEpiAct || g.mode == kEpiAccum || plain_act_grad(g));
   if (g.C2 && !(plain && g.mode == kEpiAct)) {
     set_error("gemm: the pre-activation / activation pair needs the plain activation epilogue");
+    return -1;
+  }
+  if ((g.mask_out && !(g.C2 && g.act == kActRelu && batch == 1)) || (g.mask_in && !plain_act_grad(g)) ||
+      ((g.mask_out || g.mask_in) && g.ldmask < g.N)) {
+    set_error("gemm: sign bits need a relu pre-activation / activation pair or a relu gradient, ldmask >= N");
     return -1;
   }
   // 256-row tiles for large dense plain NN products; 256-column tiles for
@@ -471,7 +561,16 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
     if (plain) hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, true, 1, 1>), grid, block, 0, s, g);  \
     else hipLaunchKernelGGL((gemm_f32_kernel<TA_, TB_, V_, false, 1, 1>), grid, block, 0, s, g);       \
   } while (0)
-  if (wide) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 2, 1>), grid, dim3(2 * NT), 0, s, g);
+  // The 256-row tiles run two workgroups per CU.  When that leaves a
+  // half-full last round but one per CU gives whole rounds (tiles = 256 mod
+  // 512 on 256 CUs, e.g. c5's batched Q/K/V projection: 768 tiles), extra
+  // dynamic LDS holds the kernel to one workgroup per CU (its static 57 KB +
+  // 32 KB > half of the CU's 160 KB): 260 -> 220 us on that projection.
+  // Otherwise two per CU are faster (c5's output layer: 1046 vs 1181 us).
+  const int64_t wide_tiles = (int64_t)entries * g.tiles_n * batch * zs;
+  const int cus = device_cus();
+  const size_t wide_dyn = wide && wide_tiles % (2 * cus) != 0 && wide_tiles % cus == 0 ? 32768 : 0;
+  if (wide) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 2, 1>), grid, dim3(2 * NT), wide_dyn, s, g);
   else if (tallg && plain) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, true, 1, 2>), grid, dim3(2 * NT), 0, s, g);
   else if (tallg) hipLaunchKernelGGL((gemm_f32_kernel<false, false, true, false, 1, 2>), grid, dim3(2 * NT), 0, s, g);
   else if (!tA && !tB) { if (vec) NSH_GEMM(false, false, true); else NSH_GEMM(false, false, false); }
@@ -513,6 +612,13 @@ int gemm_split_count(const GemmArgs& g, int batch) {
   if (!splittable(g) || g.M <= 0 || g.N <= 0 || batch <= 0) return 1;
   const int64_t tiles = ceil_div(g.M, BM) * ceil_div(g.N, BN) * batch;
   if (tiles >= 384) return 1;
+  // The largest split (chunks of at least 512) whose workgroups fill whole
+  // rounds of the CUs at up to 4 per CU (c5's output-layer weight gradient,
+  // 256 tiles: 4 chunks, 1016 us against 1032 for 3; its 512 x 512 ones: 32
+  // and 16), else enough chunks for ~768 workgroups.
+  const int cus = device_cus();
+  for (int64_t s = std::min<int64_t>(32, g.K / 512); s >= 2; s--)
+    if (tiles * s <= 4 * cus && (tiles * s) % cus == 0) return (int)ceil_div(g.K, split_chunk(g.K, (int)s));
   int64_t sp = std::min<int64_t>(ceil_div(768, tiles), g.K / 512);
   sp = std::min<int64_t>(sp, 32);
   if (sp < 2) return 1;
@@ -536,6 +642,7 @@ int launch_gemm_split(const GemmArgs& in, bool tA, bool tB, int batch, int split
   p.mode = kEpiAct;
   p.act = 0;
   p.aux = nullptr;
+  p.mask_in = nullptr;  // the reduction applies relu' from aux
   p.kchunk = chunk;
   p.sCk = n_out * batch;
   if (launch_gemm_ex(p, tA, tB, batch, s) != 0) return -1;

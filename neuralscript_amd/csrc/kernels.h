@@ -47,6 +47,24 @@ struct GemmArgs {
   // [z * kchunk, min(K, (z+1) * kchunk)) and writes C + z * sCk.
   int kchunk = 0;
   int64_t sCk = 0;
+  // ReLU sign bits, plain path only, in the MFMA accumulator layout: for
+  // the 32-row block b = row / 32, half h and column col, the 16-bit value
+  // at [(2 b + h) * ldmask + col] holds bit v = (pre-activation > 0) of row
+  // 32 b + 4 h + 8 (v / 4) + v % 4 -- the rows one lane holds.  mask_out:
+  // written by a kEpiAct GEMM with C2 set and act relu (one batch); mask_in:
+  // a relu kEpiActGrad GEMM takes the derivative from these bits instead of
+  // from aux (the same values, 1/32 of the bytes, one load per lane and
+  // block; aux stays the fallback).  Size: 2 * ceil(rows / 32) * ldmask.
+  uint16_t* mask_out = nullptr;
+  const uint16_t* mask_in = nullptr;
+  int64_t ldmask = 0;
+  // K-blocked operands (kblk > 0, a multiple of 16, float4 staging only):
+  // contraction index k lies in block k / kblk at offset k % kblk; block b of
+  // A starts at A + b * sAk and of B at B + b * sBk, each block laid out as
+  // the operand is (lda / ldb).  One launch then contracts over several
+  // separately stored products, e.g. dX = [dQ dK dV] . [Wq Wk Wv]^T.
+  int kblk = 0;
+  int64_t sAk = 0, sBk = 0;
   int tiles_m = 0, tiles_n = 0;    // filled by the launcher
 };
 

@@ -68,6 +68,7 @@ def lib():
             "nsh_objective_loss": (ci, [vp, _f32p, _f32p, sz, _f32p]),
             "nsh_profile_enable": (ci, [vp, ci]),
             "nsh_profile_reset": (ci, [vp]),
+            "nsh_profile_select": (ci, [vp, ctypes.c_char_p]),
             "nsh_profile_report": (ci, [vp, ctypes.c_char_p, sz]),
             "nsh_op_gemm": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, ci, ci, ci]),
             "nsh_op_attention_bwd_workspace": (sz, [i64, i64, i64, ci]),
@@ -273,6 +274,11 @@ class Model:
 
     def profile_reset(self):
         check(lib().nsh_profile_reset(self.h), "profile_reset")
+
+    def profile_select(self, regions=None):
+        """Time only the named profile regions (None: every region)."""
+        arg = ",".join(regions).encode() if regions else None
+        check(lib().nsh_profile_select(self.h, arg), "profile_select")
 
     def profile_report(self):
         import json
