@@ -287,6 +287,15 @@ __global__ __launch_bounds__(NT * WMW * WNW, VEC ? 4 / (WMW * WNW) : 1) void gem
     kbeg = g.kseg[blockIdx.y];
     kend = g.kseg[blockIdx.y + 1];
   }
+  if (g.kitems) {
+    if ((int)blockIdx.y >= *g.nkitems) return;
+    const int* it = g.kitems + 4 * blockIdx.y;
+    kbeg = it[1];
+    kend = it[2];
+    A = g.A;
+    B = g.B;
+    C = it[3] < 0 ? g.C + (int64_t)it[0] * g.sC : g.kpart + (int64_t)it[3] * g.sC;
+  }
   if (g.kchunk) {
     kbeg = (int)blockIdx.z * g.kchunk;
     kend = min(K, kbeg + g.kchunk);
@@ -514,7 +523,11 @@ static int device_cus() {
 int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t s) {
   if (in.M <= 0 || in.N <= 0 || batch <= 0) return 0;
   GemmArgs g = in;
-  if (g.kblk && (g.kblk % BK != 0 || g.kseg || g.groups)) {
+  if (g.kitems && (g.kseg || g.groups || g.kchunk || g.a_rows || g.c_rows || !g.nkitems)) {
+    set_error("gemm: K-chunked groups exclude the other grouping modes and row maps");
+    return -1;
+  }
+  if (g.kblk && (g.kblk % BK != 0 || g.kseg || g.kitems || g.groups)) {
     set_error("gemm: K blocks must be a multiple of 16 and exclude K-grouped and grouped modes");
     return -1;
   }
@@ -523,9 +536,9 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   // (K-grouped segments start anywhere, so a k-contiguous operand needs the
   // scalar path there.)
   const bool va = aligned16(g.A) && g.lda % 4 == 0 && g.sA % 4 == 0 && ((tA ? g.M : g.K) % 4 == 0) &&
-                  (tA || !g.kseg);
+                  (tA || !(g.kseg || g.kitems));
   const bool vb = aligned16(g.B) && g.ldb % 4 == 0 && g.sB % 4 == 0 && ((tB ? g.K : g.N) % 4 == 0) &&
-                  (!tB || !g.kseg);
+                  (!tB || !(g.kseg || g.kitems));
   const bool vec = va && vb && (!g.kblk || (g.sAk % 4 == 0 && g.sBk % 4 == 0));
   if (g.kblk && !vec) {
     set_error("gemm: K-blocked operands need 16-byte aligned, 4-float strided operands");
@@ -547,8 +560,9 @@ int launch_gemm_ex(const GemmArgs& in, bool tA, bool tB, int batch, hipStream_t 
   }
   // 256-row tiles for large dense plain NN products; 256-column tiles for
   // the grouped (per-expert) NN products, whose row ranges are short
-  const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kchunk && !g.a_rows && g.M >= 2048;
-  const bool tallg = !tA && !tB && vec && g.groups && !g.kseg && !g.kchunk && g.N >= 1024;
+  const bool wide = !tA && !tB && vec && plain && !g.groups && !g.kseg && !g.kitems && !g.kchunk && !g.a_rows &&
+                    g.M >= 2048;
+  const bool tallg = !tA && !tB && vec && g.groups && !g.kseg && !g.kitems && !g.kchunk && g.N >= 1024;
   const int bm = wide ? 2 * BM : BM, bn = tallg ? 2 * BN : BN;
   g.tiles_m = (int)ceil_div(g.M, bm);
   g.tiles_n = (int)ceil_div(g.N, bn);
@@ -601,7 +615,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 static bool splittable(const GemmArgs& g) {
-  return !g.groups && !g.kseg && !g.a_rows && !g.c_rows && !g.row_scale && !g.C2 && g.kchunk == 0;
+  return !g.groups && !g.kseg && !g.kitems && !g.a_rows && !g.c_rows && !g.row_scale && !g.C2 && g.kchunk == 0;
 }
 
 // Chunk length for `splits` chunks: a multiple of BK (and so of 4, keeping

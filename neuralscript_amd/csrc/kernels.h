@@ -43,6 +43,15 @@ struct GemmArgs {
   // K-grouped mode (kseg set): launch with batch = groups; group y contracts
   // over k in [kseg[y], kseg[y+1]) and writes C + y * sC.
   const int* kseg = nullptr;
+  // K-chunked groups (kitems set, nkitems on the device): launch with batch
+  // = an upper bound on the items; item y = kitems[4y .. 4y+3] = (group e,
+  // k begin, k end, slot) contracts over [k begin, k end) and writes
+  // C + e * sC when slot < 0, else kpart + slot * sC (a partial sum that a
+  // later pass adds up); items past *nkitems exit.  A and B are not
+  // advanced per item (the k range selects the group's rows).
+  const int* kitems = nullptr;
+  const int* nkitems = nullptr;
+  float* kpart = nullptr;
   // Split K (kchunk > 0): blockIdx.z contracts over k in
   // [z * kchunk, min(K, (z+1) * kchunk)) and writes C + z * sCk.
   int kchunk = 0;
@@ -196,7 +205,18 @@ struct MoeBwdWork {
   float* ds;       // [M, D]  dout in expert-sorted order
   float* splitk = nullptr;   // optional: K-chunk partials of dWg = x^T dg (moe_bwd_splitk_floats)
   size_t splitk_floats = 0;
+  // the expert weight gradients' work items and partial sums
+  // (moe_bwd_kitem_ints, moe_bwd_kpart_floats)
+  int* kitems = nullptr;
+  float* kpart = nullptr;
 };
+// Ints of MoeBwdWork::kitems and floats of MoeBwdWork::kpart for M tokens:
+// every expert's tokens are cut into chunks (512 tokens, more beyond 16384
+// tokens) for the weight gradients dWe1, dWe2, and the experts with several
+// chunks sum their partials in chunk order afterwards (kpart: at most 64
+// expert gradients).
+size_t moe_bwd_kitem_ints(int64_t M, int64_t E);
+size_t moe_bwd_kpart_floats(int64_t M, int64_t D, int64_t H);
 // Floats of MoeBwdWork::splitk that let dWg = x^T dg (K = M tokens, only
 // D x E outputs) run split over K; 0 when it would not be split.
 size_t moe_bwd_splitk_floats(int64_t M, int64_t D, int64_t E);

@@ -22,6 +22,8 @@
 //  * Experts: two grouped fp32-MFMA GEMMs over the expert-sorted rows: the
 //    first gathers x rows through the permutation and applies GELU in its
 //    epilogue, the second scatters rows back to token order scaled by p.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -631,16 +633,149 @@ __global__ __launch_bounds__(256) void moe_bwd_rows_kernel(const float* __restri
   for (int e = lane; e < E; e += 64) dg[(int64_t)tok * E + e] = prob_of(e) * ((e == b ? dpb : 0.f) - sd);
 }
 
-__global__ void gather_rows_kernel(const float* __restrict__ src, const int* __restrict__ perm,
-                                   const int* __restrict__ nrows, float* __restrict__ dst, int64_t D) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)(*nrows) * D) return;
-  dst[i] = src[(int64_t)perm[i / D] * D + i % D];
+// Two [M, D] arrays gathered by the same rows in one launch, W floats per
+// thread (float4 when D % 4 == 0 and the bases are 16-byte aligned):
+// dst_j[r] = src_j[perm[r]] for r < *nrows.
+template <int W>
+__global__ __launch_bounds__(256) void gather2_rows_kernel(const float* __restrict__ s1, const float* __restrict__ s2,
+                                                           const int* __restrict__ perm, const int* __restrict__ nrows,
+                                                           float* __restrict__ d1, float* __restrict__ d2, int64_t DW) {
+  typedef typename std::conditional<W == 4, float4, float>::type T;
+  const int64_t n = (int64_t)(*nrows) * DW;
+  const T* __restrict__ a = reinterpret_cast<const T*>(s1);
+  const T* __restrict__ b = reinterpret_cast<const T*>(s2);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / DW, c = i - r * DW;
+    const int64_t src = (int64_t)perm[r] * DW + c;
+    reinterpret_cast<T*>(d1)[i] = a[src];
+    reinterpret_cast<T*>(d2)[i] = b[src];
+  }
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0.f;
+}
+
+// ---- expert weight gradients in token chunks ---------------------------------
+// dWe1[e] = xs[seg e]^T dH[seg e] (and dWe2 alike) contract over the expert's
+// tokens.  Under Zipf routing one expert holds a quarter of the tokens: as one
+// K range per expert its 64 output tiles ran 4-5x longer than the rest and
+// held the launch (moep: 222 us per product against 78 us for that expert's
+// tiles alone).  Every expert's range is therefore cut into chunks of at most
+// kchunk_of(M) tokens, one GEMM work item each; an expert with one chunk writes its
+// gradient directly, one with several writes partials that
+// moe_kpart_sum_kernel adds in chunk order (deterministic).  moep's two
+// products with the partial sums: chunks of 128 tokens 0.40 ms, 256: 0.32,
+// 512: 0.29 (one range per expert: 0.49).  The chunk grows with M beyond
+// 16384 tokens so that the partial-sum buffer (its size must cover any
+// routing: 2 * ceil(M / chunk) expert gradients) stays at 64 of them.
+static int64_t kchunk_of(int64_t M) { return std::max<int64_t>(512, ceil_div(ceil_div(M, 32), 16) * 16); }
+static int64_t kitems_max(int64_t M, int64_t E) { return E + ceil_div(M, kchunk_of(M)); }
+static int64_t kreduce_max(int64_t M) { return M / (kchunk_of(M) + 1); }
+static int64_t kslots_max(int64_t M) { return 2 * ceil_div(M, kchunk_of(M)); }
+
+size_t moe_bwd_kitem_ints(int64_t M, int64_t E) {
+  return (size_t)(2 + 4 * kitems_max(M, E) + 3 * kreduce_max(M));
+}
+size_t moe_bwd_kpart_floats(int64_t M, int64_t D, int64_t H) {
+  return kreduce_max(M) > 0 ? (size_t)(kslots_max(M) * D * H) : 0;
+}
+
+// kit[0] = items, kit[1] = experts with several chunks; then maxitems items
+// (expert, k begin, k end, partial slot or -1) in expert order, then those
+// experts' (expert, first slot, chunks).  One workgroup: each thread counts
+// a run of experts; wave prefix sums (wave_incl_scan) and one LDS exchange of
+// the four wave totals turn the counts into offsets.
+
+__global__ __launch_bounds__(256) void moe_kitems_kernel(const int* __restrict__ seg, int E, int kc, int maxitems,
+                                                         int* __restrict__ kit) {
+  __shared__ int wtot[3][4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, per = (E + 255) / 256;
+  const int e0 = min(E, t * per), e1 = min(E, e0 + per);
+  auto chunks = [&](int e) {
+    const int n = seg[e + 1] - seg[e];
+    return n > kc ? (n + kc - 1) / kc : 1;
+  };
+  int cnt[3] = {0, 0, 0};  // items, partial slots, experts with several chunks
+  for (int e = e0; e < e1; e++) {
+    const int c = chunks(e);
+    cnt[0] += c;
+    if (c > 1) {
+      cnt[1] += c;
+      cnt[2]++;
+    }
+  }
+  int incl[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    incl[j] = wave_incl_scan(cnt[j]);
+    if (lane == 63) wtot[j][w] = incl[j];
+  }
+  __syncthreads();
+  int off[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    int before = 0;
+    for (int u = 0; u < w; u++) before += wtot[j][u];
+    off[j] = before + incl[j] - cnt[j];
+  }
+  if (t == 255) {
+    kit[0] = off[0] + cnt[0];
+    kit[1] = off[2] + cnt[2];
+  }
+  int io = off[0], so = off[1], ro = off[2];
+  int* items = kit + 2;
+  int* red = kit + 2 + 4 * maxitems;
+  for (int e = e0; e < e1; e++) {
+    const int c = chunks(e), b0 = seg[e], b1 = seg[e + 1];
+    for (int z = 0; z < c; z++, io++) {
+      items[4 * io] = e;
+      items[4 * io + 1] = b0 + z * kc;
+      items[4 * io + 2] = min(b1, b0 + (z + 1) * kc);
+      items[4 * io + 3] = c > 1 ? so + z : -1;
+    }
+    if (c > 1) {
+      red[3 * ro] = e;
+      red[3 * ro + 1] = so;
+      red[3 * ro + 2] = c;
+      ro++;
+      so += c;
+    }
+  }
+}
+
+// C[e] = sum over its chunks z (in order) of kpart[first slot + z]; blockIdx.y
+// = entry of an expert with several chunks (entries past kit[1] exit).  VEC:
+// float4 elements (DH % 4 == 0; the buffers are 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(256) void moe_kpart_sum_kernel(const int* __restrict__ kit, int maxitems,
+                                                            const float* __restrict__ kpart, float* __restrict__ C,
+                                                            int64_t DH) {
+  const int r = blockIdx.y;
+  if (r >= kit[1]) return;
+  const int* red = kit + 2 + 4 * maxitems + 3 * r;
+  const int e = red[0], s0 = red[1], c = red[2];
+  const float* __restrict__ src = kpart + (int64_t)s0 * DH;
+  float* __restrict__ dst = C + (int64_t)e * DH;
+  if (VEC) {
+    const int64_t n4 = DH / 4;
+    const float4* __restrict__ s4 = reinterpret_cast<const float4*>(src);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256) {
+      float4 a = s4[i];
+      for (int z = 1; z < c; z++) {
+        const float4 b = s4[(int64_t)z * n4 + i];
+        a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+      }
+      reinterpret_cast<float4*>(dst)[i] = a;
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < DH; i += (int64_t)gridDim.x * 256) {
+      float a = src[i];
+      for (int z = 1; z < c; z++) a += src[(int64_t)z * DH + i];
+      dst[i] = a;
+    }
+  }
 }
 
 // dWg[D, E] = x[M, D]^T dg[M, E]
@@ -708,26 +843,57 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
   }
   if (!(phases & kMoeBwdKGrouped)) return 0;
   // expert-sorted copies of x and dout for the K-grouped products
-  const dim3 gd((unsigned)ceil_div(M * D, 256));
-  hipLaunchKernelGGL(gather_rows_kernel, gd, dim3(256), 0, s, x, w.perm, nrows, b.xs, D);
-  hipLaunchKernelGGL(gather_rows_kernel, gd, dim3(256), 0, s, dout, w.perm, nrows, b.ds, D);
+  const bool gvec = D % 4 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dout) |
+                      reinterpret_cast<uintptr_t>(b.xs) | reinterpret_cast<uintptr_t>(b.ds)) & 15) == 0;
+  const int64_t DW = gvec ? D / 4 : D;
+  const dim3 gd((unsigned)std::min<int64_t>(ceil_div(M * DW, 256), 8192));
+  if (gvec)
+    hipLaunchKernelGGL(gather2_rows_kernel<4>, gd, dim3(256), 0, s, x, dout, w.perm, nrows, b.xs, b.ds, DW);
+  else
+    hipLaunchKernelGGL(gather2_rows_kernel<1>, gd, dim3(256), 0, s, x, dout, w.perm, nrows, b.xs, b.ds, DW);
   NSH_LAUNCHED();
-  if (dWe1) {  // dWe1[e] [D, H] = xs[seg e]^T dH[seg e]
-    GemmArgs k;
-    k.A = b.xs; k.B = b.dH; k.C = dWe1;
-    k.M = (int)D; k.N = (int)H; k.K = (int)M;
-    k.lda = D; k.ldb = H; k.ldc = H;
-    k.kseg = w.seg; k.sC = D * H;
-    if (launch_gemm_ex(k, true, false, (int)E, s) != 0) return -1;
+  // token chunks of each expert (without the work buffers: one K range per
+  // expert)
+  const bool chunked = b.kitems && (b.kpart || kreduce_max(M) == 0);
+  const int maxitems = (int)kitems_max(M, E), maxred = (int)kreduce_max(M);
+  if (chunked) {
+    hipLaunchKernelGGL(moe_kitems_kernel, dim3(1), dim3(256), 0, s, w.seg, (int)E, (int)kchunk_of(M), maxitems,
+                       b.kitems);
+    NSH_LAUNCHED();
   }
-  if (dWe2) {  // dWe2[e] [H, D] = hp[seg e]^T ds[seg e]
+  auto weight_grad = [&](const float* A, const float* B, float* C, int64_t R, int64_t Cc) -> int {
     GemmArgs k;
-    k.A = b.hp; k.B = b.ds; k.C = dWe2;
-    k.M = (int)H; k.N = (int)D; k.K = (int)M;
-    k.lda = H; k.ldb = D; k.ldc = D;
-    k.kseg = w.seg; k.sC = H * D;
-    if (launch_gemm_ex(k, true, false, (int)E, s) != 0) return -1;
-  }
+    k.A = A; k.B = B; k.C = C;
+    k.M = (int)R; k.N = (int)Cc; k.K = (int)M;
+    k.lda = R; k.ldb = Cc; k.ldc = Cc;
+    k.sC = R * Cc;
+    if (!chunked) {
+      k.kseg = w.seg;
+      return launch_gemm_ex(k, true, false, (int)E, s);
+    }
+    k.kitems = b.kitems + 2; k.nkitems = b.kitems; k.kpart = b.kpart;
+    if (launch_gemm_ex(k, true, false, maxitems, s) != 0) return -1;
+    if (maxred > 0) {
+      const int64_t DH = R * Cc;
+      const bool vec = DH % 4 == 0 && ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(b.kpart)) & 15) == 0;
+      // one element (float4) per thread: each entry's sum is a few MB, and
+      // fewer threads looping over it left the pass latency-bound
+      const unsigned gx = (unsigned)std::min<int64_t>(ceil_div(vec ? DH / 4 : DH, 256), 4096);
+      if (vec)
+        hipLaunchKernelGGL(moe_kpart_sum_kernel<true>, dim3(gx, maxred), dim3(256), 0, s, b.kitems, maxitems, b.kpart,
+                           C, DH);
+      else
+        hipLaunchKernelGGL(moe_kpart_sum_kernel<false>, dim3(gx, maxred), dim3(256), 0, s, b.kitems, maxitems, b.kpart,
+                           C, DH);
+      NSH_LAUNCHED();
+    }
+    return 0;
+  };
+  // dWe1[e] [D, H] = xs[seg e]^T dH[seg e]
+  if (dWe1 && weight_grad(b.xs, b.dH, dWe1, D, H) != 0) return -1;
+  // dWe2[e] [H, D] = hp[seg e]^T ds[seg e]
+  if (dWe2 && weight_grad(b.hp, b.ds, dWe2, H, D) != 0) return -1;
   return 0;
 }
 

@@ -612,53 +612,100 @@ __global__ __launch_bounds__(256) void emb_grad_rows_vec_kernel(const float* __r
 }
 
 // ---- embedding weight gradient in one launch (no sort, no workspace) --------
-// Each workgroup owns 16 * RPW consecutive vocabulary rows.  It reads every
-// token id once (the ids are shared by all workgroups, so they come from L2)
-// and marks the tokens that hit its rows in one LDS bitmap per row, bit t =
-// token t.  Walking a row's bitmap word by word and bit by bit visits its
-// tokens in ascending order, so each output element is the reference's
-// sequential sum with no sort at all.  Each wave owns RPW rows (rows wv,
-// wv + 16, ...): it gathers a row's tokens' gradient rows (kEmbAhead loads in
-// flight) and adds them in token order, then writes the dW row once (zeros if
-// no token).  Two rows per wave halve the workgroups that each scan all ids
-// (c5's 16384 ids over 8192 rows: 18.3 -> 15.2 us); they are used when the
-// grid still holds a workgroup per CU.
+// G = 2^lg workgroups; workgroup b owns the vocabulary rows b, b + G, b + 2G,
+// ... (16 * RPW of them; strided, so that the frequent ids, which cluster at
+// the low ids of a vocabulary, land on different CUs).  It reads every token
+// id once (the ids are shared by all workgroups, so they come from L2) and
+// marks the tokens that hit its rows in one LDS bitmap per row, bit t =
+// token t, counting each row's tokens.  Walking a row's bitmap word by word
+// and bit by bit visits its tokens in ascending order, so each output
+// element is the reference's sequential sum with no sort at all.  Each wave
+// owns RPW rows: it gathers a row's tokens' gradient rows (kEmbAhead loads in
+// flight) and adds them in token order, then writes the dW row once (zeros
+// if no token).  Two rows per wave halve the workgroups that each scan all
+// ids (c5's 16384 ids over 8192 rows: 18.3 -> 15.2 us); they are used when
+// the grid still holds a workgroup per CU.
 constexpr int kEmbWaves = 16;  // 16 waves of 64 lanes
 // LDS budget of the bitmaps: 16 * RPW * ceil(n/32) words (128 KB at RPW 2).
 constexpr int64_t kEmbFusedMaxTokens = 32768;
+// A float4 row hit by more than kEmbHeavy tokens is summed by the whole
+// workgroup instead: one wave's chain of gathers would hold the launch (a
+// Zipf-distributed batch put ~2900 of 16384 ids on row 0: 1.6 ms).  Its
+// tokens are listed in order in LDS, kEmbList at a time.
+constexpr int kEmbHeavy = 64;
+constexpr int kEmbList = 2048;
+// LDS words of the fused kernel: bitmaps, per-row token counts, token list,
+// per-wave sums.
+static size_t emb_fused_lds_words(int64_t n, int rows) {
+  return (size_t)rows * (size_t)((n + 31) >> 5) + (size_t)rows + (size_t)kEmbList + kEmbWaves;
+}
+
+// Value of lane (lane + S) of the same 16-lane row (lane + S stays in the
+// row for the lanes that use the result).
+template <int S>
+__device__ __forceinline__ float row_shl(float v) {
+  if constexpr (S == 0) return v;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + S, 0xF, 0xF, false));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_prefix_sum(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
 
 template <bool VEC, int NV, int kEmbAhead, bool VEC_IDX, int RPW>
 __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __restrict__ dout,
                                                               const float* __restrict__ idx,
                                                               float* __restrict__ dW, int64_t n, int64_t V,
-                                                              int64_t D) {
+                                                              int64_t D, int lg) {
   constexpr int kRows = kEmbWaves * RPW;
   extern __shared__ unsigned emb_bits[];
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int nw = (int)((n + 31) >> 5);
-  const int64_t r0 = (int64_t)blockIdx.x * kRows;
-  for (int i = t; i < kRows * nw; i += 1024) emb_bits[i] = 0u;
+  const int b = blockIdx.x, gmask = (1 << lg) - 1;
+  int* const row_cnt = reinterpret_cast<int*>(emb_bits + kRows * nw);  // tokens per local row
+  int* const tok_list = row_cnt + kRows;                                 // kEmbList ints
+  int* const wsum = tok_list + kEmbList;                                 // kEmbWaves ints
+  // the first batch of ids is in flight while the bitmaps are cleared
+  const float4* __restrict__ idx4 = reinterpret_cast<const float4*>(idx);
+  const int64_t n4 = n >> 2;
+  float4 f0[4];
+  if (VEC_IDX) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int64_t j = (int64_t)k * 1024 + t;
+      f0[k] = j < n4 ? idx4[j] : make_float4(-1.f, -1.f, -1.f, -1.f);
+    }
+  }
+  for (int i = t; i < kRows * nw + kRows; i += 1024) emb_bits[i] = 0u;
   __syncthreads();
-  // A token is this workgroup's when emb_row(id) lies in [r0, r0 + rows):
-  // tested in float, exactly (the bounds are integers below 2^24), as
-  // id >= r0 (id > -1 for r0 = 0: ids in (-1, 0) truncate to row 0) and
-  // id < min(r0 + rows, V); NaN fails both.  The row is then the truncation.
-  const bool first = r0 == 0;
-  const float lo = first ? -1.0f : (float)r0;
-  const float hi = (float)(r0 + kRows < V ? r0 + kRows : V);
+  // A token hits row (int)id when -1 < id < V (exact in float: V <= 2^24;
+  // ids in (-1, 0) truncate to row 0; NaN fails both tests).  Row g is local
+  // row g >> lg of workgroup g & (G - 1).
+  const float vhi = (float)V;
   auto mark = [&](float f, int64_t i) {
-    if ((first ? f > lo : f >= lo) && f < hi)
-      atomicOr(&emb_bits[((int)f - (int)r0) * nw + (int)(i >> 5)], 1u << (i & 31));
+    if (f > -1.0f && f < vhi) {
+      const int g = (int)f;
+      if ((g & gmask) == b) {
+        const int row = g >> lg;
+        atomicOr(&emb_bits[row * nw + (int)(i >> 5)], 1u << (i & 31));
+        atomicAdd(&row_cnt[row], 1);
+      }
+    }
   };
   if (VEC_IDX) {  // float4 of ids, 4 per thread in flight, then the n % 4 tail
-    const float4* __restrict__ idx4 = reinterpret_cast<const float4*>(idx);
-    const int64_t n4 = n >> 2;
     for (int64_t base = 0; base < n4; base += 4 * 1024) {
       float4 f[4];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         const int64_t j = base + k * 1024 + t;
-        f[k] = j < n4 ? idx4[j] : make_float4(-1.f, -1.f, -1.f, -1.f);
+        f[k] = base == 0 ? f0[k] : j < n4 ? idx4[j] : make_float4(-1.f, -1.f, -1.f, -1.f);
       }
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -680,13 +727,18 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
     }
   }
   __syncthreads();
+  // Local rows the whole workgroup sums (float4 rows only): one bit each,
+  // the same mask in every wave.
+  const uint64_t heavy = VEC ? __ballot(lane < kRows && row_cnt[lane] > kEmbHeavy) : 0ull;
   // Columns per pass: 64 lanes x NV float4 (VEC) or 64 lanes x NV floats.
   constexpr int W = VEC ? 4 : 1;
   const int64_t DW = D / W;
   for (int rr = 0; rr < RPW; rr++) {
-    const int64_t r = r0 + wv + kEmbWaves * rr;
-    if (r >= V) return;
-    const unsigned* __restrict__ bits = emb_bits + (wv + kEmbWaves * rr) * nw;
+    const int j = wv + kEmbWaves * rr;
+    const int64_t r = b + ((int64_t)j << lg);
+    if (r >= V) break;
+    if ((heavy >> j) & 1) continue;  // the workgroup's, below
+    const unsigned* __restrict__ bits = emb_bits + j * nw;
     // The pass loop is wave-uniform (every lane takes part in the ballots and
     // lane reads below); lanes past the row's end only skip their loads/stores.
     for (int64_t cb = 0; cb < DW; cb += 64 * NV) {
@@ -694,20 +746,20 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
       float acc[NV][W];
       float buf[kEmbAhead][NV][W];
 #pragma unroll
-      for (int j = 0; j < NV; j++)
+      for (int jj = 0; jj < NV; jj++)
 #pragma unroll
-        for (int k = 0; k < W; k++) acc[j][k] = 0.f;
+        for (int k = 0; k < W; k++) acc[jj][k] = 0.f;
       int pend = 0;  // loads in flight, oldest in slot (head % kEmbAhead)
       int head = 0;
       auto add_oldest = [&]() {
-        const int s = head % kEmbAhead;
+        const int sl = head % kEmbAhead;
 #pragma unroll
         for (int q = 0; q < kEmbAhead; q++)
-          if (q == s)
+          if (q == sl)
 #pragma unroll
-            for (int j = 0; j < NV; j++)
+            for (int jj = 0; jj < NV; jj++)
 #pragma unroll
-              for (int k = 0; k < W; k++) acc[j][k] += buf[q][j][k];
+              for (int k = 0; k < W; k++) acc[jj][k] += buf[q][jj][k];
         head++;
         pend--;
       };
@@ -719,28 +771,28 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
           nz &= nz - 1;
           unsigned wd = (unsigned)__builtin_amdgcn_readlane((int)word, l);
           while (wd) {
-            const int b = __builtin_ctz(wd);
+            const int bt = __builtin_ctz(wd);
             wd &= wd - 1;
-            const int64_t tok = (int64_t)(w0 + l) * 32 + b;
+            const int64_t tok = (int64_t)(w0 + l) * 32 + bt;
             if (pend == kEmbAhead) add_oldest();
-            const int s = (head + pend) % kEmbAhead;
+            const int sl = (head + pend) % kEmbAhead;
             const float* src = dout + tok * D;
 #pragma unroll
             for (int q = 0; q < kEmbAhead; q++)
-              if (q == s)
+              if (q == sl)
 #pragma unroll
-                for (int j = 0; j < NV; j++) {
-                  const int64_t c = c0 + 64 * j;
+                for (int jj = 0; jj < NV; jj++) {
+                  const int64_t c = c0 + 64 * jj;
                   if (c < DW) {
                     if constexpr (VEC) {
                       const float4 v = reinterpret_cast<const float4*>(src)[c];
-                      buf[q][j][0] = v.x; buf[q][j][1] = v.y; buf[q][j][2] = v.z; buf[q][j][3] = v.w;
+                      buf[q][jj][0] = v.x; buf[q][jj][1] = v.y; buf[q][jj][2] = v.z; buf[q][jj][3] = v.w;
                     } else {
-                      buf[q][j][0] = src[c];
+                      buf[q][jj][0] = src[c];
                     }
                   } else {
 #pragma unroll
-                    for (int k = 0; k < W; k++) buf[q][j][k] = 0.f;
+                    for (int k = 0; k < W; k++) buf[q][jj][k] = 0.f;
                   }
                 }
             pend++;
@@ -750,14 +802,95 @@ __global__ __launch_bounds__(1024) void emb_grad_fused_kernel(const float* __res
       while (pend > 0) add_oldest();
       float* o = dW + r * D;
 #pragma unroll
-      for (int j = 0; j < NV; j++) {
-        const int64_t c = c0 + 64 * j;
+      for (int jj = 0; jj < NV; jj++) {
+        const int64_t c = c0 + 64 * jj;
         if (c < DW) {
           if constexpr (VEC)
-            reinterpret_cast<float4*>(o)[c] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+            reinterpret_cast<float4*>(o)[c] = make_float4(acc[jj][0], acc[jj][1], acc[jj][2], acc[jj][3]);
           else
-            o[c] = acc[j][0];
+            o[c] = acc[jj][0];
         }
+      }
+    }
+  }
+  if constexpr (VEC) {
+    // Heavy rows, one after another, by all 16 waves.  Thread t holds bitmap
+    // word t (n <= 32768 tokens: at most 1024 words) and the rank of its first
+    // token; segments of kEmbList tokens are listed in order in LDS.  Wave w
+    // takes column groups g = w, w + 16, ... of 8 float4; lane = 8 c + s loads
+    // column 8 g + c of the token in slot s of a round of 8 consecutive tokens
+    // (8 tokens x 128 B per load instruction), and the lanes with s = 0 add
+    // the 8 slots in order (row_shl by s within the 16-lane row), so each
+    // element is still the sequential sum in token order.  Rounds go 8 at a
+    // time with the next 8 rounds' loads in flight.
+    const int c = lane >> 3, sl = lane & 7;
+    const int64_t G = (DW + 7) / 8;
+    uint64_t hm = heavy;
+    while (hm) {
+      const int j = __builtin_ctzll(hm);
+      hm &= hm - 1;
+      const int64_t r = b + ((int64_t)j << lg);
+      const int total = row_cnt[j];
+      const unsigned word = t < nw ? emb_bits[j * nw + t] : 0u;
+      const int pc = __popc(word);
+      const int incl = wave_prefix_sum(pc);
+      __syncthreads();  // wsum of the previous heavy row has been read
+      if (lane == 63) wsum[wv] = incl;
+      __syncthreads();
+      int first = incl - pc;
+      for (int u = 0; u < wv; u++) first += wsum[u];
+      for (int64_t g0 = 0; g0 < G; g0 += kEmbWaves) {
+        const int64_t col = (g0 + wv) * 8 + c;  // this lane's float4 column
+        const bool cin = g0 + wv < G && col < DW;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int seg = 0; seg < total; seg += kEmbList) {
+          __syncthreads();  // the previous segment's list has been read
+          if (word && first < seg + kEmbList && first + pc > seg) {
+            int rk = first;
+            for (unsigned wd = word; wd; wd &= wd - 1, rk++)
+              if (rk >= seg && rk < seg + kEmbList) tok_list[rk - seg] = t * 32 + __builtin_ctz(wd);
+          }
+          __syncthreads();
+          const int cnt = min(kEmbList, total - seg);
+          const int nr = (cnt + 7) / 8;
+          auto load_round = [&](int rd) {
+            const int k = rd * 8 + sl;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (cin && rd < nr && k < cnt) v = reinterpret_cast<const float4*>(dout + (int64_t)tok_list[k] * D)[col];
+            return v;
+          };
+          float4 cur[8], nxt[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) cur[u] = load_round(u);
+          for (int bt = 0; bt < nr; bt += 8) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) nxt[u] = load_round(bt + 8 + u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              const int base = (bt + u) * 8;  // the round's first token
+              const float4 v = cur[u];
+#define NSH_ADD_SLOT(S)       \
+  if (base + S < cnt) {       \
+    acc.x += row_shl<S>(v.x); \
+    acc.y += row_shl<S>(v.y); \
+    acc.z += row_shl<S>(v.z); \
+    acc.w += row_shl<S>(v.w); \
+  }
+              NSH_ADD_SLOT(0)
+              NSH_ADD_SLOT(1)
+              NSH_ADD_SLOT(2)
+              NSH_ADD_SLOT(3)
+              NSH_ADD_SLOT(4)
+              NSH_ADD_SLOT(5)
+              NSH_ADD_SLOT(6)
+              NSH_ADD_SLOT(7)
+#undef NSH_ADD_SLOT
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+          }
+        }
+        if (cin && sl == 0) reinterpret_cast<float4*>(dW + r * D)[col] = acc;
       }
     }
   }
@@ -772,30 +905,40 @@ __global__ __launch_bounds__(256) void fill_zero_ints_kernel(int* __restrict__ p
 // Workspace: ints [V] count, [V+1] start, [V] cursor, [n] order, [n] tmp.
 size_t embedding_grad_workspace(int64_t n, int64_t V) { return (size_t)(3 * V + 1 + 2 * n); }
 
+// Rows per wave: 2 while that still leaves a workgroup for each of the 256
+// CUs, else 1.  Workgroups: the power of two G >= ceil(V / rows per group).
+static int emb_grad_rows_per_wave(int64_t V) { return ceil_div(V, 2 * kEmbWaves) >= 256 ? 2 : 1; }
+static int emb_grad_lg(int64_t V) {
+  const int64_t need = ceil_div(V, (int64_t)kEmbWaves * emb_grad_rows_per_wave(V));
+  int lg = 0;
+  while (((int64_t)1 << lg) < need) lg++;
+  return lg;
+}
+
 // One launch without workspace when the bitmaps fit in LDS, the
 // workgroups' shared reads of the ids stay small (n ids per workgroup) and
 // row numbers are exact in float (V <= 2^24).
 static bool emb_grad_fused_fits(int64_t n, int64_t V) {
-  return n <= kEmbFusedMaxTokens && V <= ((int64_t)1 << 24) && n * ceil_div(V, kEmbWaves) <= ((int64_t)1 << 26);
+  return n <= kEmbFusedMaxTokens && V <= ((int64_t)1 << 24) && (n << emb_grad_lg(V)) <= ((int64_t)1 << 26);
 }
-
-// Rows per wave: 2 while that still leaves a workgroup for each of the 256
-// CUs, else 1.
-static int emb_grad_rows_per_wave(int64_t V) { return ceil_div(V, 2 * kEmbWaves) >= 256 ? 2 : 1; }
 
 template <bool VEC, bool VEC_IDX, int RPW>
 static void launch_emb_grad_fused_rpw(const float* dout, const float* idx, float* dW, int64_t n, int64_t V, int64_t D,
                                       hipStream_t s) {
-  const dim3 g((unsigned)ceil_div(V, kEmbWaves * RPW));
-  const size_t lds = (size_t)kEmbWaves * RPW * (size_t)((n + 31) >> 5) * sizeof(unsigned);
+  const int lg = emb_grad_lg(V);
+  const dim3 g(1u << lg);
+  const size_t lds = emb_fused_lds_words(n, kEmbWaves * RPW) * sizeof(unsigned);
   const int64_t DW = VEC ? D / 4 : D;
   // NV columns per lane per pass, AH rows in flight: NV * AH float4 of loads
   if (DW > 128)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 4, 2, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D,
+                       lg);
   else if (DW > 64)
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 2, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D,
+                       lg);
   else
-    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D);
+    hipLaunchKernelGGL((emb_grad_fused_kernel<VEC, 1, 4, VEC_IDX, RPW>), g, dim3(1024), lds, s, dout, idx, dW, n, V, D,
+                       lg);
 }
 
 template <bool VEC, bool VEC_IDX>

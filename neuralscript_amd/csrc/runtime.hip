@@ -1034,6 +1034,10 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
               b.splitk_floats = moe_bwd_splitk_floats(M, q.D, q.E);
               b.splitk = b.splitk_floats ? scratch(m, "moe_splitk", b.splitk_floats) : nullptr;
               if (b.splitk_floats && !b.splitk) return -1;
+              b.kitems = reinterpret_cast<int*>(scratch(m, "moe_kitems", moe_bwd_kitem_ints(M, q.E)));
+              const size_t nkp = moe_bwd_kpart_floats(M, q.D, q.H);
+              b.kpart = nkp ? scratch(m, "moe_kpart", nkp) : nullptr;
+              if (!b.kitems || (nkp && !b.kpart)) return -1;
               moe_dx = scratch(m, "moe_gx", (size_t)(M * q.D));
               moe_dwg = scratch(m, "moe_gwg", (size_t)(q.D * q.E));
               moe_dwe1 = scratch(m, "moe_gwe1", (size_t)(q.E * q.D * q.H));

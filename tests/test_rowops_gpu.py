@@ -73,20 +73,36 @@ def test_activation_backward(act):
                                         (4096, 64, 512, "same"), (20000, 300, 1024, "skew"),
                                         (5000, 20000, 64, "uniform"), (32768, 8191, 1000, "uniform"),
                                         (0, 37, 8, "uniform"), (40000, 8192, 512, "uniform"),
-                                        (50000, 300, 64, "skew"), (33000, 17, 20, "same")])
+                                        (50000, 300, 64, "skew"), (33000, 17, 20, "same"),
+                                        (16384, 8192, 512, "zipf"), (16384, 8192, 512, "heavy65"),
+                                        (32768, 8191, 1000, "skew"), (12000, 700, 60, "skew"),
+                                        (9000, 100, 21, "zipf")])
 def test_embedding_grad_is_bit_exact(n, V, D, mode):
     """Row sums in ascending token order, float4 columns (D % 4 == 0: one,
     two or four float4 per lane) or scalar ones.  Up to 32768 tokens one
-    launch walks per-row token bitmaps (32768: the bitmaps fill 64 KB of LDS;
-    no tokens: every row zero); beyond, the counting-sort path: short
-    segments sorted per thread, long ones (one row taking every token;
-    several heavy rows in one block under skewed ids) by the workgroup."""
+    launch walks per-row token bitmaps (32768: the bitmaps fill 128 KB of
+    LDS; no tokens: every row zero), and a float4 row hit by more than 64
+    tokens is summed by the whole workgroup, 8 tokens per load, in token
+    order (one row taking every token, Zipf-distributed ids, rows of exactly
+    64 and 65 tokens, partial column groups at D = 60 and 1000); beyond 32768
+    tokens, the counting-sort path: short segments sorted per thread, long
+    ones (one row taking every token; several heavy rows in one block under
+    skewed ids) by the workgroup."""
     print(f"embedding_grad n={n} V={V} D={D} {mode}", flush=True)
     if mode == "same":
         idx = np.full(n, 3.0, np.float32)   # one row takes every token
     elif mode == "skew":
         # a few rows take most tokens: segments of hundreds to thousands
         idx = np.minimum(np.random.default_rng(13).pareto(1.1, n), V - 1).astype(np.int64).astype(np.float32)
+    elif mode == "zipf":
+        # word-frequency-like ids: row 0 takes ~18% of the tokens
+        idx = np.minimum(np.random.default_rng(14).zipf(1.2, n) - 1, V - 1).astype(np.float32)
+    elif mode == "heavy65":
+        # rows 5 and 6 (one workgroup) hit by exactly 64 and 65 tokens, row 40
+        # (another) by 65, the rest uniform over rows >= 64
+        idx = synth.token_ids(11, n, V - 64) + 64
+        pos = np.random.default_rng(15).permutation(n)[:194]
+        idx[pos[:64]], idx[pos[64:129]], idx[pos[129:]] = 5, 6, 40
     else:
         idx = synth.token_ids(11, n, V)
     if mode == "edge":
