@@ -190,6 +190,14 @@ struct Frame {
   // pitch, written by the training forward's GEMM for the backward's relu'
   // epilogue (GemmArgs::mask_out / mask_in)
   std::map<int, std::pair<uint16_t*, int64_t>> relu_bits;
+  // a value the caller's buffer receives directly (the device-pointer
+  // forward's return value), or -1; not when that buffer would overlap the
+  // input [direct_in, direct_in + direct_in_n), which the producing
+  // instruction may still read
+  int direct_id = -1;
+  float* direct = nullptr;
+  const float* direct_in = nullptr;
+  size_t direct_in_n = 0;
 };
 
 float* scratch(ns_model* m, const std::string& key, size_t n) {
@@ -263,6 +271,12 @@ void keep_frame(ns_model* m, const Frame& fr) {
 }
 
 float* out_buf(ns_model* m, Frame& fr, int id, size_t n) {
+  if (id == fr.direct_id &&
+      (fr.direct + n <= fr.direct_in || fr.direct_in + fr.direct_in_n <= fr.direct)) {
+    fr.numel[id] = n;
+    fr.ptr[id] = fr.direct;
+    return fr.direct;
+  }
   if (ensure(m->arena[id], n) != 0) return nullptr;
   fr.numel[id] = n;
   fr.ptr[id] = m->arena[id].p;
@@ -555,7 +569,10 @@ int exec_forward_op(ns_model* m, const Func& F, const Instr& I, Frame& fr, bool 
 
 int ensure_device_current(ns_model* m);
 
-int run_forward(ns_model* m, const float* d_x, size_t n_in, float** d_out, size_t* n_out) {
+// direct (optional): the caller's output buffer, which the instruction that
+// produces the return value then writes itself (no copy afterwards), unless
+// it overlaps the input (out_buf).
+int run_forward(ns_model* m, const float* d_x, size_t n_in, float** d_out, size_t* n_out, float* direct = nullptr) {
   if (ensure_device_current(m) != 0) return -1;
   const Plan& P = *m->plan;
   const Func& F = P.fwd;
@@ -563,17 +580,26 @@ int run_forward(ns_model* m, const float* d_x, size_t n_in, float** d_out, size_
   bind_weights(m, fr);
   fr.numel[F.x] = n_in;
   fr.ptr[F.x] = const_cast<float*>(d_x);
+  if (direct && F.ret >= 0 && F.ret != F.x) {
+    fr.direct_id = F.ret;
+    fr.direct = direct;
+    fr.direct_in = d_x;
+    fr.direct_in_n = n_in;
+  }
   for (const Instr& I : F.ins) {
     if (I.fused_away || I.op == Op::Marker) continue;
     if (exec_forward_op(m, F, I, fr, false) != 0) return -1;
   }
-  keep_frame(m, fr);
   if (F.ret < 0) {
+    keep_frame(m, fr);
     set_error("forward function has no return value");
     return -1;
   }
   *d_out = fr.ptr[F.ret];
   *n_out = fr.numel[F.ret];
+  // the caller's buffer is not the model's to read back later
+  if (fr.direct_id >= 0 && fr.ptr[F.ret] == direct) fr.ptr[F.ret] = nullptr;
+  keep_frame(m, fr);
   return 0;
 }
 
@@ -1292,8 +1318,9 @@ int nsh_eval_infer_device(ns_model* m, const float* d_input, float* d_output, si
   }
   float* res = nullptr;
   size_t n = 0;
-  if (run_forward(m, d_input, input_numel, &res, &n) != 0) return -1;
-  if (n) NSH_CHECK(hipMemcpyAsync(d_output, res, n * sizeof(float), hipMemcpyDeviceToDevice, m->stream));
+  if (run_forward(m, d_input, input_numel, &res, &n, d_output) != 0) return -1;
+  if (n && res != d_output)
+    NSH_CHECK(hipMemcpyAsync(d_output, res, n * sizeof(float), hipMemcpyDeviceToDevice, m->stream));
   return 0;
 }
 

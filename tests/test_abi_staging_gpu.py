@@ -8,6 +8,7 @@ import pytest
 
 import helpers
 import oracle
+from golden.make_golden import CASES, case_inputs
 from neuralscript_amd import runtime, synth, workloads
 
 pytestmark = pytest.mark.gpu
@@ -63,3 +64,40 @@ def test_train_step_host_equals_device_path_and_weights_read_back():
     assert helpers.bitwise_equal(c.get_weights(), w), "staged weight read-back differs from the blob"
     for mm in (a, b, c):
         mm.free()
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c[0])
+def test_device_forward_writes_the_callers_buffer(case):
+    """The device-pointer forward has the instruction that produces the
+    return value write the caller's output buffer itself (no copy after the
+    forward); the host-pointer forward keeps the model's own buffer and
+    copies it out.  Both must agree bit for bit (outputs pre-filled with NaN:
+    some data-movement programs write fewer values than the output size),
+    and so must a device call whose output buffer is the input buffer (the
+    library then falls back to its own buffer and a copy, as the last
+    instruction may still read the input)."""
+    name, rows, seed = case[:3]
+    print(f"device forward {name} rows={rows}", flush=True)
+    ir = helpers.ir_text(name)
+    plan = runtime.Plan(ir)
+    net, x, _ = case_inputs(name, rows, seed)
+    w = helpers.net_weights(name, seed)
+    m = runtime.Model(plan, w)
+    try:
+        n_out = plan.output_numel(x.size)
+        host = np.full(n_out, np.nan, np.float32)
+        m.eval_infer(x, out=host)
+        dx, dout = DA.from_host(x), DA.from_host(np.full(n_out, np.nan, np.float32))
+        m.eval_infer_device(dx, dout)
+        m.sync()
+        assert helpers.bitwise_equal(host, dout.to_host()), f"{name}: device forward differs from the host path"
+        both_h = np.full(max(n_out, x.size), np.nan, np.float32)
+        both_h[:x.size] = x
+        both = DA.from_host(both_h)
+        runtime.check(runtime.lib().nsh_eval_infer_device(m.h, both.ptr, both.ptr, x.size), "eval in place")
+        m.sync()
+        got = both.to_host()[:n_out]
+        written = ~np.isnan(host)
+        assert helpers.bitwise_equal(host[written], got[written]), f"{name}: in-place device forward differs"
+    finally:
+        m.free()
