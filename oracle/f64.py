@@ -21,7 +21,13 @@ GPU's blocked ones) can be measured against a common yardstick:
   dS = P (dp - rowsum(P dp)), dQ = dS K scale, dV = P^T dPre, dK = dS^T Q
   scale; dW* = x^T d*, dWo = oh^T dout, dX = dQ Wq^T + dK Wk^T + dV Wv^T);
 * cross-entropy mean over rows of -sum_{y>0} log p (:1598-1613) and its
-  gradient (p - y) / rows (:1582-1595).
+  gradient (p - y) / rows (:1582-1595);
+* the top-1 mixture of experts, forward (:1915-1945: p = softmax of the
+  live experts' gate logits, out = p_best GELU(x We1[best]) We2[best], GELU
+  with erf and the float32 constant 0.70710678f) and its four gradients
+  (:1388-1579), with each token's expert taken from the float32 oracle's
+  routing (`moe_best`): float64 logits could break a near tie the other
+  way, and the choice is a discrete decision, not a rounding error.
 
 The instruction walk follows oracle.Model._run (the reference's train core,
 codegen.cpp:2755-3157) for the subset of operations above; anything else
@@ -178,10 +184,70 @@ def loss_grad(preds, labels, C):
     return ((p - labels.reshape(-1, C)) / p.shape[0]).ravel()
 
 
-def train_values(net, w, x, y):
+_MOE_C = F64(np.float32(0.7071067811865476))   # the emitted GELU's 1/sqrt(2)
+_MOE_C2 = F64(np.float32(0.3989422804014327))  # and its 1/sqrt(2 pi)
+
+
+def _moe_probs(X, Wg, live):
+    lg = X @ Wg
+    mx = np.where(live, lg, -np.inf).max(axis=1, keepdims=True)
+    ex = np.where(live, np.exp(lg - mx), 0.0)
+    return ex / ex.sum(axis=1, keepdims=True)
+
+
+def moe_fwd(x, Wg, We1, We2, live, best, D, H, E):
+    """or_moe_fwd's formula in float64 with the given expert per token
+    (best < 0: no live expert, zero output)."""
+    X = x.reshape(-1, D)
+    Wg, We1, We2 = Wg.reshape(D, E), We1.reshape(E, D, H), We2.reshape(E, H, D)
+    p = _moe_probs(X, Wg, live)
+    out = np.zeros_like(X)
+    for e in np.unique(best[best >= 0]):
+        t = best == e
+        u = X[t] @ We1[e]
+        out[t] = p[t, e][:, None] * ((0.5 * u * (1.0 + _erf(u * _MOE_C))) @ We2[e])
+    return out.ravel()
+
+
+def moe_bwd(dout, x, Wg, We1, We2, live, best, D, H, E):
+    """or_moe_bwd's formulas in float64: (dx, dWg, dWe1, dWe2).  Per token
+    with expert b: u = x We1[b], dp = We2[b] dout, g = GELU(u), g' = GELU'(u),
+    dpb = g . dp, dH = dp p_b g', dG_e = p_e ([e = b] dpb - dpb p_b);
+    dx = dG Wg^T + dH We1[b]^T, dWg = x^T dG, dWe1[b] = x^T dH,
+    dWe2[b] = (p_b g)^T dout over the tokens of b."""
+    X, G = x.reshape(-1, D), dout.reshape(-1, D)
+    M = X.shape[0]
+    Wg, We1, We2 = Wg.reshape(D, E), We1.reshape(E, D, H), We2.reshape(E, H, D)
+    p = _moe_probs(X, Wg, live)
+    DG = np.zeros((M, E))
+    dx = np.zeros((M, D))
+    dWe1, dWe2 = np.zeros((E, D, H)), np.zeros((E, H, D))
+    for e in np.unique(best[best >= 0]):
+        t = np.nonzero(best == e)[0]
+        u = X[t] @ We1[e]
+        dp = G[t] @ We2[e].T
+        er = _erf(u * _MOE_C)
+        g = 0.5 * u * (1.0 + er)
+        gd = 0.5 * (1.0 + er) + u * np.exp(-u * u * 0.5) * _MOE_C2
+        pb = p[t, e]
+        dpb = np.sum(g * dp, axis=1)
+        dH = dp * pb[:, None] * gd
+        DG[t] = p[t] * (-(dpb * pb)[:, None])
+        DG[t, e] += p[t, e] * dpb
+        dx[t] = dH @ We1[e].T
+        dWe1[e] = X[t].T @ dH
+        dWe2[e] = (g * pb[:, None]).T @ G[t]
+    dx += DG @ Wg.T
+    return dx.ravel(), (X.T @ DG).ravel(), dWe1.ravel(), dWe2.ravel()
+
+
+def train_values(net, w, x, y, moe_best=None):
     """Every value of one training step's forward and reverse bodies of
     `net` (an oracle.Net) at weights `w`, ids/inputs `x` and one-hot labels
-    `y`, in float64: (values by IR id, loss).  The optimizer is not run."""
+    `y`, in float64: (values by IR id, loss).  The optimizer is not run.
+    A MoE network needs `moe_best`, the float32 oracle's expert per token
+    (record["moe_best"] of oracle.Model.train_step); its initial K0 experts
+    are the live ones."""
     f = net.train
     wset = set(net.shape)
     w = np.asarray(w, np.float32).astype(F64)
@@ -263,6 +329,27 @@ def train_values(net, w, x, y):
         elif op == "ns.grad.embedding.w":
             V, D = net.shape[o[2]]
             buf[i.result] = embedding_grad(val(o[0]), xs if o[1] == xid else val(o[1]), V, D)
+        elif op == "ns.layer.moe":
+            m = net.moe
+            if moe_best is None:
+                raise NotImplementedError("float64 MoE needs the oracle's routing (moe_best)")
+            live = np.zeros(m["E"], bool)
+            live[:m["K0"]] = True
+            best = np.asarray(moe_best)
+            buf[i.result] = moe_fwd(val(o[0]), *(weight(n) for n in o[1:4]), live, best, m["D"], m["H"], m["E"])
+            width[i.result] = m["D"]
+        elif op.startswith("ns.grad.moe."):
+            m = net.moe
+            key = ("moe", o[0], o[1])
+            if key not in buf:
+                live = np.zeros(m["E"], bool)
+                live[:m["K0"]] = True
+                buf[key] = moe_bwd(val(o[0]), val(o[1]), *(weight(n) for n in o[2:5]), live,
+                                   np.asarray(moe_best), m["D"], m["H"], m["E"])
+            which = {"x": 0, "wg": 1, "we1": 2, "we2": 3}[op.split(".")[-1]]
+            buf[i.result] = buf[key][which]
+            if which == 0:
+                width[i.result] = m["D"]
         elif op.startswith("ns.grad.attention."):
             key = ("attn", o[0], o[1], o[2])
             if key not in buf:
