@@ -209,6 +209,12 @@ struct MoeBwdWork {
   // (moe_bwd_kitem_ints, moe_bwd_kpart_floats)
   int* kitems = nullptr;
   float* kpart = nullptr;
+  // optional, with kitems: one int per expert, nonzero when its dWe1 / dWe2
+  // slices may hold nonzeros.  An expert without tokens then gets its zero
+  // gradients written only when its flag is set (and the flag cleared); an
+  // expert with tokens sets it.  The caller keeps the array with the two
+  // gradient buffers and sets every flag when either buffer is new.
+  int* dirty = nullptr;
 };
 // Ints of MoeBwdWork::kitems and floats of MoeBwdWork::kpart for M tokens:
 // every expert's tokens are cut into chunks (512 tokens, more beyond 16384

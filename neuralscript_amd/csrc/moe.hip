@@ -689,13 +689,15 @@ size_t moe_bwd_kpart_floats(int64_t M, int64_t D, int64_t H) {
 // the four wave totals turn the counts into offsets.
 
 __global__ __launch_bounds__(256) void moe_kitems_kernel(const int* __restrict__ seg, int E, int kc, int maxitems,
-                                                         int* __restrict__ kit) {
+                                                         int* __restrict__ kit, int* __restrict__ dirty) {
   __shared__ int wtot[3][4];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, per = (E + 255) / 256;
   const int e0 = min(E, t * per), e1 = min(E, e0 + per);
+  // an expert without tokens: one empty item (its zero gradients), or none
+  // when its slices are known to be zero already
   auto chunks = [&](int e) {
     const int n = seg[e + 1] - seg[e];
-    return n > kc ? (n + kc - 1) / kc : 1;
+    return n > kc ? (n + kc - 1) / kc : n > 0 || !dirty || dirty[e] ? 1 : 0;
   };
   int cnt[3] = {0, 0, 0};  // items, partial slots, experts with several chunks
   for (int e = e0; e < e1; e++) {
@@ -743,6 +745,10 @@ __global__ __launch_bounds__(256) void moe_kitems_kernel(const int* __restrict__
       so += c;
     }
   }
+  // after both passes over this thread's experts: which slices the launch
+  // leaves nonzero (only this thread touches its experts' flags)
+  if (dirty)
+    for (int e = e0; e < e1; e++) dirty[e] = seg[e + 1] > seg[e] ? 1 : 0;
 }
 
 // C[e] = sum over its chunks z (in order) of kpart[first slot + z]; blockIdx.y
@@ -859,7 +865,7 @@ int launch_moe_backward(const float* x, const float* dout, const float* Wg, cons
   const int maxitems = (int)kitems_max(M, E), maxred = (int)kreduce_max(M);
   if (chunked) {
     hipLaunchKernelGGL(moe_kitems_kernel, dim3(1), dim3(256), 0, s, w.seg, (int)E, (int)kchunk_of(M), maxitems,
-                       b.kitems);
+                       b.kitems, b.dirty);
     NSH_LAUNCHED();
   }
   auto weight_grad = [&](const float* A, const float* B, float* C, int64_t R, int64_t Cc) -> int {

@@ -68,6 +68,9 @@ struct ns_model {
   std::map<int, std::vector<uint8_t>> drop_keep;  // host staging of each dropout's keep flags
   int64_t lr_step = 0;
   int64_t moe_last_m = 0;         // tokens routed by the last MoE forward
+  // the expert weight gradients' per-expert nonzero flags and the buffers
+  // they describe (MoeBwdWork::dirty)
+  const void* moe_dirty_for[3] = {nullptr, nullptr, nullptr};
   struct Adam {
     float* m = nullptr;
     float* v = nullptr;
@@ -1071,6 +1074,17 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
               if (!w.pre || !b.dpre2 || !b.dH || !b.hp || !b.dg || !b.xs || !b.ds || !moe_dx || !moe_dwg ||
                   !moe_dwe1 || !moe_dwe2)
                 return -1;
+              // per-expert flags: all set when the flags or either gradient
+              // buffer is new (fresh memory holds anything)
+              b.dirty = reinterpret_cast<int*>(scratch(m, "moe_dirty", (size_t)q.E));
+              if (!b.dirty) return -1;
+              if (m->moe_dirty_for[0] != b.dirty || m->moe_dirty_for[1] != moe_dwe1 ||
+                  m->moe_dirty_for[2] != moe_dwe2) {
+                NSH_CHECK(hipMemsetAsync(b.dirty, 1, (size_t)q.E * sizeof(int), s));
+                m->moe_dirty_for[0] = b.dirty;
+                m->moe_dirty_for[1] = moe_dwe1;
+                m->moe_dirty_for[2] = moe_dwe2;
+              }
               // three profile regions: the expert-grouped products (dpre2 and
               // dx), the router gradient, the K-grouped weight gradients
               static const std::pair<const char*, int> kPhases[] = {

@@ -373,3 +373,44 @@ def test_moe_training_step_with_many_experts(E, rows):
             ref = rec["buf"][ins.result]
             helpers.assert_close(model.read_value(ins.result, ref.size), ref, f"{ins.op} E={E}")
     model.free()
+
+
+def test_expert_gradients_after_a_step_that_routed_elsewhere():
+    """The expert weight gradients of an expert without tokens are zeros,
+    written only when that expert's slices may hold something (a per-expert
+    flag kept with the gradient buffers).  A step on a 3-token batch right
+    after a step on 64 tokens that used other experts must give exactly the
+    gradients of the same 3-token step on a fresh model (lr 0: the weights do
+    not move), the stale slices of the first step's experts cleared."""
+    name = "moet"
+    print(f"moe gradients after rerouting ({name})", flush=True)
+    ir = helpers.ir_text(name)
+    net = oracle.Net(ir)
+    E = net.moe["E"]
+    w = helpers.net_weights_for(net, 811)
+    xa, ya = helpers.net_inputs(net, name, 812, 64), helpers.net_labels(net, 812, 64)
+    xb, yb = helpers.net_inputs(net, name, 813, 3), helpers.net_labels(net, 813, 3)
+    plan = runtime.Plan(ir)
+    grads = [i.result for i in net.train.instrs if i.op.startswith("ns.grad.moe.")]
+    sizes = {i.result: i for i in net.train.instrs if i.op.startswith("ns.grad.moe.")}
+    om = oracle.Model(net, w)
+    om._opt_step = lambda *a, **k: None
+    rec = {}
+    om.train_step(xb, yb, 0.0, rec)
+    m1 = runtime.Model(plan, w)
+    m1.train_step(xa, ya, 0.0)
+    used_a = set(m1.last_routing(64, E)[0].tolist())
+    m1.train_step(xb, yb, 0.0)
+    used_b = set(m1.last_routing(3, E)[0].tolist())
+    assert used_a - used_b, "the first batch must use experts the second does not"
+    m2 = runtime.Model(plan, w)
+    m2.train_step(xb, yb, 0.0)
+    try:
+        for g in grads:
+            n = rec["buf"][g].size
+            a, b = m1.read_value(g, n), m2.read_value(g, n)
+            assert helpers.bitwise_equal(a, b), f"{sizes[g].op} after rerouting differs from a fresh model's"
+            helpers.assert_close(a, rec["buf"][g], sizes[g].op)
+    finally:
+        m1.free()
+        m2.free()
