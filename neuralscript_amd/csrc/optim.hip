@@ -281,6 +281,57 @@ __device__ __forceinline__ float* slice_dots(const MuonMat& M) { return M.red + 
 __device__ __forceinline__ float* slice_dot_totals(const MuonMat& M) {
   return slice_dots(M) + (size_t)kSlicePanel * M.C * mgs_slices(M.R);
 }
+__device__ __forceinline__ int* slice_live(const MuonMat& M) {
+  return reinterpret_cast<int*>(slice_dot_totals(M) + (size_t)kSlicePanel * M.C);
+}
+
+// Vectors past the last nonzero one (c >= the returned count) are exactly
+// zero, and stay so: every projection onto them and of them is 0 * q, and
+// each normalises to 0 / (0 + 1e-30) = 0 -- they need no work at all, and
+// the others' results do not depend on them (a gradient of MoE expert
+// weights holds zero rows for the experts without tokens).  The count is
+// the maximum over the slices' counts (mgs_slice_live_kernel), the same in
+// every workgroup.
+__device__ __forceinline__ int slice_live_count(const MuonMat& M) {
+  const int* __restrict__ lv = slice_live(M);
+  const int nsl = mgs_slices(M.R);
+  int m = 0;
+  for (int i = threadIdx.x & 63; i < nsl; i += 64) m = max(m, lv[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o));
+  return m;
+}
+
+// Each slice's count of vectors up to its last nonzero one, from the last
+// vector down (a slice stops at its first nonzero element).
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_live_kernel(const MuonMat* __restrict__ mats, int nmat);
+
+__global__ __launch_bounds__(kSliceThreads) void mgs_slice_live_kernel(const MuonMat* __restrict__ mats, int nmat) {
+  __shared__ int any[4];
+  int mi, b;
+  if (!slice_of(mats, nmat, mi, b)) return;
+  const MuonMat& M = mats[mi];
+  const SliceIO io(M, b);
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  int n = 0;
+  for (int c = M.C - 1; c >= 0; c--) {
+    float x[kSliceEPT];
+    io.load(c, x);
+    bool nz = false;
+#pragma unroll
+    for (int e = 0; e < kSliceEPT; e++) nz |= x[e] != 0.f;
+    const bool wnz = __ballot(nz) != 0;
+    if (lane == 0) any[w] = wnz;
+    __syncthreads();
+    const bool found = any[0] | any[1] | any[2] | any[3];
+    __syncthreads();
+    if (found) {
+      n = c + 1;
+      break;
+    }
+  }
+  if (t == 0) slice_live(M)[b] = n;
+}
 
 // One column step of the sliced path inside a panel ending at column cend,
 // over every long matrix; j = -1 only writes column 0's partials.
@@ -294,8 +345,8 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), ce = min(C, cend);
-  if (j >= C) return;
+  const int C = M.C, nsl = mgs_slices(M.R), nlive = slice_live_count(M), ce = min(nlive, cend);
+  if (j >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float* __restrict__ Pin = M.red + (size_t)(j & 1) * C * nsl;
   float* __restrict__ Pout = M.red + (size_t)((j + 1) & 1) * C * nsl;
@@ -365,16 +416,16 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_dots_kernel(const Muo
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
-  if (j1 >= C) return;
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
+  if (j1 >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const SliceIO io(M, b);
   float* __restrict__ pd = slice_dots(M);
   float q[kSlicePanel][kSliceEPT];
 #pragma unroll
   for (int k = 0; k < kSlicePanel; k++) io.load(j0 + k, q[k]);
-  for (int c0 = j1; c0 < C; c0 += kDotBatch) {
-    const int nb = min(kDotBatch, C - c0);
+  for (int c0 = j1; c0 < nlive; c0 += kDotBatch) {
+    const int nb = min(kDotBatch, nlive - c0);
     float x[kDotBatch][kSliceEPT];
 #pragma unroll
     for (int u = 0; u < kDotBatch; u++) {
@@ -410,10 +461,10 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_dots_kernel(const Muo
 __global__ __launch_bounds__(256) void mgs_slice_reduce_kernel(const MuonMat* __restrict__ mats, int nmat, int j0) {
   const MuonMat& M = mats[blockIdx.y];
   if (M.R <= kMaxPanelR) return;
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
   const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int k = p / C, c = p % C;
-  if (j1 >= C || k >= kSlicePanel || c < j1) return;
+  if (j1 >= nlive || k >= kSlicePanel || c < j1 || c >= nlive) return;
   const float v = slice_total(slice_dots(M) + ((size_t)k * C + c) * nsl, nsl);
   if ((threadIdx.x & 63) == 0) slice_dot_totals(M)[(size_t)k * C + c] = v;
   (void)nmat;
@@ -430,8 +481,8 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_update_kernel(const M
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel;
-  if (j1 >= C) return;
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
+  if (j1 >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const SliceIO io(M, b);
   const float* __restrict__ dd = slice_dot_totals(M);
@@ -439,8 +490,8 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_update_kernel(const M
   float q[kSlicePanel][kSliceEPT];
 #pragma unroll
   for (int k = 0; k < kSlicePanel; k++) io.load(j0 + k, q[k]);
-  for (int c0 = j1; c0 < C; c0 += kSliceBatch) {
-    const int nb = min(kSliceBatch, C - c0);
+  for (int c0 = j1; c0 < nlive; c0 += kSliceBatch) {
+    const int nb = min(kSliceBatch, nlive - c0);
     float x[kSliceBatch][kSliceEPT];
 #pragma unroll
     for (int u = 0; u < kSliceBatch; u++) {
@@ -829,8 +880,11 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
 int64_t mgs_max_panel_len() { return kMaxPanelR; }
 
 size_t mgs_red_floats(int64_t R, int64_t C) {
-  // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl] and their totals [kSlicePanel][C]
-  return R > kMaxPanelR ? (size_t)((2 + kSlicePanel) * C * (int64_t)mgs_slices(R) + kSlicePanel * C) : 0;
+  // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl], their
+  // totals [kSlicePanel][C], and each slice's count of vectors up to its
+  // last nonzero one [nsl] (ints)
+  return R > kMaxPanelR ? (size_t)((2 + kSlicePanel) * C * (int64_t)mgs_slices(R) + kSlicePanel * C + mgs_slices(R))
+                        : 0;
 }
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
@@ -874,6 +928,8 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
   // panel's raw dots with every later vector, their totals, and the
   // projections of every later vector (which also start the next panel).
   if (slices > 0) {
+    hipLaunchKernelGGL(mgs_slice_live_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat);
+    NSH_LAUNCHED();
     hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, -1, kSlicePanel);
     NSH_LAUNCHED();
   }

@@ -118,11 +118,14 @@ def test_muon_multi_matches_oracle(shapes):
         helpers.assert_close(dw[i].to_host(), ref, f"muon multi matrix {i} {r}x{c}")
 
 
-@pytest.mark.parametrize("r,c,zero", [(24, 9000, (3, 10, 17)), (20000, 19, (0, 8, 18))])
+@pytest.mark.parametrize("r,c,zero", [(24, 9000, (3, 10, 17)), (20000, 19, (0, 8, 18)),
+                                      (32, 30000, tuple(range(20, 32))), (40000, 24, (5,) + tuple(range(9, 24)))])
 def test_sliced_orthonormalize_with_zero_vectors(r, c, zero):
     """Zero gradient vectors (a MoE expert without tokens) on the sliced
     path: MGS's +1e-30 guard gives them q = 0, in the panel that holds them
-    and as projections of the later panels; everything else as the oracle."""
+    and as projections of the later panels; everything else as the oracle.
+    Trailing zero vectors (the last 12 of 32, the last 15 of 24) are not
+    processed at all (a slice scan finds the last nonzero vector)."""
     print(f"mgs zero vectors {r}x{c} {zero}", flush=True)
     g = synth.normal(r * 5 + c, r * c).reshape(r, c)
     for z in zero:
