@@ -17,6 +17,9 @@
 //    tiles never leave registers.
 //  * exp2 with scores pre-multiplied by scale*log2(e); the final 1/l and the
 //    transpose back to row-major go through LDS for coalesced stores.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -720,10 +723,341 @@ __global__ __launch_bounds__(256) void attn_delta_rows_kernel(const float* __res
   }
 }
 
+// Head sizes above 128 (the wide path): the scores of a block of query rows
+// are materialised as [H][rows][S] by the MFMA GEMM kernels, and these row
+// kernels apply the reference's per-row arithmetic to them
+// (codegen.cpp:1746-1766 forward, :1868-1873 backward).  One workgroup per
+// row; VEC: the row length is a multiple of 4 (rows 16-byte aligned).
+
+// Sum or max over the 256 threads; every thread gets the result.
+template <bool MAX>
+__device__ __forceinline__ float wide_block_reduce(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o, 64);
+    v = MAX ? fmaxf(v, u) : v + u;
+  }
+  __syncthreads();  // earlier readers of red are done
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = red[0];
+#pragma unroll
+  for (int i = 1; i < 4; i++) v = MAX ? fmaxf(v, red[i]) : v + red[i];
+  return v;
+}
+
+// Row r of P (the raw dots q . k) becomes softmax(dots * scale): the scaled
+// score rounded as the reference stores it, exp(score - max), divided by the
+// row's sum.  lse (optional): row r = h * nq + i writes lse[h * S + q0 + i]
+// in the flash kernels' log2 units.
+template <bool VEC>
+__global__ __launch_bounds__(256) void wide_softmax_kernel(float* __restrict__ P, int S, float scale,
+                                                           float* __restrict__ lse, int nq, int q0) {
+#pragma clang fp contract(off)
+  __shared__ float red[4];
+  float* __restrict__ row = P + (int64_t)blockIdx.x * S;
+  const int t = threadIdx.x;
+  float m = -INFINITY, l = 0.f;
+  if constexpr (VEC) {
+    float4* r4 = reinterpret_cast<float4*>(row);
+    const int n4 = S / 4;
+    for (int j = t; j < n4; j += 256) {
+      const float4 a = r4[j];
+      m = fmaxf(fmaxf(m, fmaxf(a.x * scale, a.y * scale)), fmaxf(a.z * scale, a.w * scale));
+    }
+    m = wide_block_reduce<true>(m, red);
+    for (int j = t; j < n4; j += 256) {
+      const float4 a = r4[j];
+      const float4 e = make_float4(expf(a.x * scale - m), expf(a.y * scale - m), expf(a.z * scale - m),
+                                   expf(a.w * scale - m));
+      r4[j] = e;
+      l += e.x + e.y + e.z + e.w;
+    }
+    l = wide_block_reduce<false>(l, red);
+    for (int j = t; j < n4; j += 256) {
+      const float4 e = r4[j];
+      r4[j] = make_float4(e.x / l, e.y / l, e.z / l, e.w / l);
+    }
+  } else {
+    for (int j = t; j < S; j += 256) m = fmaxf(m, row[j] * scale);
+    m = wide_block_reduce<true>(m, red);
+    for (int j = t; j < S; j += 256) {
+      const float e = expf(row[j] * scale - m);
+      row[j] = e;
+      l += e;
+    }
+    l = wide_block_reduce<false>(l, red);
+    for (int j = t; j < S; j += 256) row[j] = row[j] / l;
+  }
+  if (lse && t == 0) {
+    const int h = blockIdx.x / nq, i = blockIdx.x % nq;
+    lse[(int64_t)h * S + q0 + i] = m * 1.4426950408889634f + log2f(l);
+  }
+}
+
+// The same two row kernels with the row held in registers, for rows of up
+// to 16 K floats that are a multiple of 4 (one read and one write of each
+// element instead of three reads and two writes): 1024 threads, float4
+// chunks t + 1024 i, i < EPT / 4.
+template <bool MAX>
+__device__ __forceinline__ float wide_block_reduce16(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float u = __shfl_xor(v, o, 64);
+    v = MAX ? fmaxf(v, u) : v + u;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = red[0];
+#pragma unroll
+  for (int i = 1; i < 16; i++) v = MAX ? fmaxf(v, red[i]) : v + red[i];
+  return v;
+}
+
+template <int EPT>
+__global__ __launch_bounds__(1024) void wide_softmax_reg_kernel(float* __restrict__ P, int S, float scale,
+                                                                float* __restrict__ lse, int nq, int q0) {
+#pragma clang fp contract(off)
+  __shared__ float red[16];
+  float4* __restrict__ r4 = reinterpret_cast<float4*>(P + (int64_t)blockIdx.x * S);
+  const int t = threadIdx.x, n4 = S / 4;
+  float4 x[EPT / 4];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPT / 4; i++) {
+    const int c = t + 1024 * i;
+    x[i] = c < n4 ? r4[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (c < n4) m = fmaxf(fmaxf(m, fmaxf(x[i].x * scale, x[i].y * scale)), fmaxf(x[i].z * scale, x[i].w * scale));
+  }
+  m = wide_block_reduce16<true>(m, red);
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPT / 4; i++)
+    if (t + 1024 * i < n4) {
+      x[i] = make_float4(expf(x[i].x * scale - m), expf(x[i].y * scale - m), expf(x[i].z * scale - m),
+                         expf(x[i].w * scale - m));
+      l += x[i].x + x[i].y + x[i].z + x[i].w;
+    }
+  l = wide_block_reduce16<false>(l, red);
+#pragma unroll
+  for (int i = 0; i < EPT / 4; i++) {
+    const int c = t + 1024 * i;
+    if (c < n4) r4[c] = make_float4(x[i].x / l, x[i].y / l, x[i].z / l, x[i].w / l);
+  }
+  if (lse && t == 0) {
+    const int h = blockIdx.x / nq, i = blockIdx.x % nq;
+    lse[(int64_t)h * S + q0 + i] = m * 1.4426950408889634f + log2f(l);
+  }
+}
+
+template <int EPT>
+__global__ __launch_bounds__(1024) void wide_dsoftmax_reg_kernel(const float* __restrict__ P, float* __restrict__ G,
+                                                                 int S, float scale) {
+#pragma clang fp contract(off)
+  __shared__ float red[16];
+  const int64_t off = (int64_t)blockIdx.x * S;
+  const float4* __restrict__ p4 = reinterpret_cast<const float4*>(P + off);
+  float4* __restrict__ g4 = reinterpret_cast<float4*>(G + off);
+  const int t = threadIdx.x, n4 = S / 4;
+  float4 a[EPT / 4], b[EPT / 4];
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPT / 4; i++) {
+    const int c = t + 1024 * i;
+    if (c < n4) {
+      a[i] = p4[c];
+      b[i] = g4[c];
+      dot += a[i].x * b[i].x + a[i].y * b[i].y + a[i].z * b[i].z + a[i].w * b[i].w;
+    }
+  }
+  dot = wide_block_reduce16<false>(dot, red);
+#pragma unroll
+  for (int i = 0; i < EPT / 4; i++) {
+    const int c = t + 1024 * i;
+    if (c < n4)
+      g4[c] = make_float4(a[i].x * (b[i].x - dot) * scale, a[i].y * (b[i].y - dot) * scale,
+                          a[i].z * (b[i].z - dot) * scale, a[i].w * (b[i].w - dot) * scale);
+  }
+}
+
+// Row r of G (dP = dO V^T) becomes scale * P o (dP - sum_j P dP): dS with
+// the 1/sqrt(dk) of dQ and dK folded in.
+template <bool VEC>
+__global__ __launch_bounds__(256) void wide_dsoftmax_kernel(const float* __restrict__ P, float* __restrict__ G, int S,
+                                                            float scale) {
+#pragma clang fp contract(off)
+  __shared__ float red[4];
+  const int64_t off = (int64_t)blockIdx.x * S;
+  const float* __restrict__ p = P + off;
+  float* __restrict__ g = G + off;
+  const int t = threadIdx.x;
+  float dot = 0.f;
+  if constexpr (VEC) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4* g4 = reinterpret_cast<float4*>(g);
+    const int n4 = S / 4;
+    for (int j = t; j < n4; j += 256) {
+      const float4 a = p4[j], b = g4[j];
+      dot += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    }
+    dot = wide_block_reduce<false>(dot, red);
+    for (int j = t; j < n4; j += 256) {
+      const float4 a = p4[j], b = g4[j];
+      g4[j] = make_float4(a.x * (b.x - dot) * scale, a.y * (b.y - dot) * scale, a.z * (b.z - dot) * scale,
+                          a.w * (b.w - dot) * scale);
+    }
+  } else {
+    for (int j = t; j < S; j += 256) dot += p[j] * g[j];
+    dot = wide_block_reduce<false>(dot, red);
+    for (int j = t; j < S; j += 256) g[j] = p[j] * (g[j] - dot) * scale;
+  }
+}
+
 }  // namespace
 
-// The tiled kernels' head sizes; others are padded to the next one.
+// The tiled kernels' head sizes; others up to 128 are padded to the next one.
 static int64_t padded_dk(int64_t dk) { return dk <= 32 ? 32 : dk <= 64 ? 64 : dk <= 128 ? 128 : 0; }
+
+// Query rows per block of the wide path: all S when H * S * S floats fit
+// 1 GiB, else as many as do (at least one).  The environment variable
+// NSHIP_ATTN_WIDE_ROWS (a positive integer) lowers it, so that small cases
+// can run several blocks.
+static int64_t wide_rows(int64_t S, int64_t H) {
+  constexpr int64_t kWideFloats = int64_t(1) << 28;
+  int64_t r = std::max<int64_t>(1, std::min<int64_t>(S, kWideFloats / std::max<int64_t>(1, H * S)));
+  if (const char* e = getenv("NSHIP_ATTN_WIDE_ROWS")) {
+    const long long v = atoll(e);
+    if (v > 0) r = std::min<int64_t>(r, v);
+  }
+  return r;
+}
+
+// P V (forward) and dS K (backward dQ) of a block of nq query rows:
+// [nq, S] x [S, dk] per head.  K = S is long and the output has few tiles,
+// so they split K (gemm_split_count) through a workspace placed after the
+// score buffers, at a 64-float boundary.
+static GemmArgs wide_pv_args(int64_t nq, int64_t S, int64_t dk) {
+  GemmArgs g;
+  g.M = (int)nq; g.N = (int)dk; g.K = (int)S;
+  return g;
+}
+
+static size_t wide_split_floats(int64_t S, int64_t H, int64_t dk) {
+  const int64_t rows = wide_rows(S, H);
+  size_t m = 0;
+  for (const int64_t nq : {rows, S % rows})
+    if (nq > 0) {
+      const GemmArgs g = wide_pv_args(nq, S, dk);
+      m = std::max(m, gemm_split_workspace(g, (int)H, gemm_split_count(g, (int)H)));
+    }
+  return m;
+}
+
+static int64_t wide_score_floats(int64_t S, int64_t H, bool backward) {
+  return ((backward ? 2 : 1) * H * wide_rows(S, H) * S + 63) / 64 * 64;
+}
+
+// Scores of query rows q0 .. q0 + nq of every head: P[h] = Q_h K_h^T (raw
+// dots), [H][nq][S].
+static int wide_scores(const float* Q, const float* K, float* P, int64_t q0, int64_t nq, int64_t S, int64_t H,
+                       int64_t dk, int64_t ld, hipStream_t s) {
+  GemmArgs g;
+  g.A = Q + q0 * ld; g.lda = ld; g.sA = dk;
+  g.B = K; g.ldb = ld; g.sB = dk;
+  g.C = P; g.ldc = S; g.sC = nq * S;
+  g.M = (int)nq; g.N = (int)S; g.K = (int)dk;
+  return launch_gemm_ex(g, false, true, (int)H, s);
+}
+
+// Elements per thread of the register-resident row kernels (0: the row does
+// not fit, or is not a whole number of 16-byte aligned float4).
+static int wide_reg_ept(int64_t S, const void* a, const void* b) {
+  if (S % 4 != 0 || (reinterpret_cast<uintptr_t>(a) & 15) || (reinterpret_cast<uintptr_t>(b) & 15)) return 0;
+  return S <= 4096 ? 4 : S <= 8192 ? 8 : S <= 16384 ? 16 : 0;
+}
+
+static int wide_softmax(float* P, int64_t q0, int64_t nq, int64_t S, int64_t H, float scale, float* lse,
+                        hipStream_t s) {
+  const bool vec = S % 4 == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0;
+  const dim3 grid((unsigned)(H * nq)), block(256), big(1024);
+  switch (wide_reg_ept(S, P, P)) {
+    case 4: hipLaunchKernelGGL(wide_softmax_reg_kernel<4>, grid, big, 0, s, P, (int)S, scale, lse, (int)nq, (int)q0); break;
+    case 8: hipLaunchKernelGGL(wide_softmax_reg_kernel<8>, grid, big, 0, s, P, (int)S, scale, lse, (int)nq, (int)q0); break;
+    case 16: hipLaunchKernelGGL(wide_softmax_reg_kernel<16>, grid, big, 0, s, P, (int)S, scale, lse, (int)nq, (int)q0); break;
+    default:
+      if (vec) hipLaunchKernelGGL(wide_softmax_kernel<true>, grid, block, 0, s, P, (int)S, scale, lse, (int)nq, (int)q0);
+      else hipLaunchKernelGGL(wide_softmax_kernel<false>, grid, block, 0, s, P, (int)S, scale, lse, (int)nq, (int)q0);
+  }
+  NSH_LAUNCHED();
+  return 0;
+}
+
+// ctx = P V per block of query rows.
+static int wide_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t H,
+                    int64_t dk, int64_t ld, float scale, float* ws, hipStream_t s) {
+  const int64_t rows = wide_rows(S, H);
+  for (int64_t q0 = 0; q0 < S; q0 += rows) {
+    const int64_t nq = std::min(rows, S - q0);
+    if (wide_scores(Q, K, ws, q0, nq, S, H, dk, ld, s) || wide_softmax(ws, q0, nq, S, H, scale, lse, s)) return -1;
+    GemmArgs g = wide_pv_args(nq, S, dk);
+    g.A = ws; g.lda = S; g.sA = nq * S;
+    g.B = V; g.ldb = ld; g.sB = dk;
+    g.C = ctx + q0 * ld; g.ldc = ld; g.sC = dk;
+    if (launch_gemm_split(g, false, false, (int)H, gemm_split_count(g, (int)H), ws + wide_score_floats(S, H, false), s))
+      return -1;
+  }
+  return 0;
+}
+
+// Per block of query rows: P again (as the forward computes it), G = dO V^T,
+// G = scale * dS, then dV += P^T dO, dK += G^T Q (both summed over the
+// blocks in order) and dQ = G K for the block's rows.
+static int wide_bwd(const float* Q, const float* K, const float* V, const float* dO, float* dQ, float* dK, float* dV,
+                    int64_t S, int64_t H, int64_t dk, int64_t ld, float scale, float* ws, hipStream_t s) {
+  const int64_t rows = wide_rows(S, H);
+  float *P = ws, *G = ws + H * rows * S;
+  const bool vec = S % 4 == 0 && (reinterpret_cast<uintptr_t>(G) & 15) == 0 && (reinterpret_cast<uintptr_t>(P) & 15) == 0;
+  for (int64_t q0 = 0; q0 < S; q0 += rows) {
+    const int64_t nq = std::min(rows, S - q0);
+    if (wide_scores(Q, K, P, q0, nq, S, H, dk, ld, s) || wide_softmax(P, q0, nq, S, H, scale, nullptr, s)) return -1;
+    GemmArgs g;
+    g.A = dO + q0 * ld; g.lda = ld; g.sA = dk;
+    g.B = V; g.ldb = ld; g.sB = dk;
+    g.C = G; g.ldc = S; g.sC = nq * S;
+    g.M = (int)nq; g.N = (int)S; g.K = (int)dk;
+    if (launch_gemm_ex(g, false, true, (int)H, s)) return -1;
+    const dim3 grid((unsigned)(H * nq)), block(256), big(1024);
+    switch (wide_reg_ept(S, P, G)) {
+      case 4: hipLaunchKernelGGL(wide_dsoftmax_reg_kernel<4>, grid, big, 0, s, P, G, (int)S, scale); break;
+      case 8: hipLaunchKernelGGL(wide_dsoftmax_reg_kernel<8>, grid, big, 0, s, P, G, (int)S, scale); break;
+      case 16: hipLaunchKernelGGL(wide_dsoftmax_reg_kernel<16>, grid, big, 0, s, P, G, (int)S, scale); break;
+      default:
+        if (vec) hipLaunchKernelGGL(wide_dsoftmax_kernel<true>, grid, block, 0, s, P, G, (int)S, scale);
+        else hipLaunchKernelGGL(wide_dsoftmax_kernel<false>, grid, block, 0, s, P, G, (int)S, scale);
+    }
+    NSH_LAUNCHED();
+    const float* lhs[2] = {P, G};
+    const float* rhs[2] = {dO + q0 * ld, Q + q0 * ld};
+    float* out[2] = {dV, dK};
+    for (int i = 0; i < 2; i++) {
+      GemmArgs t;
+      t.A = lhs[i]; t.lda = S; t.sA = nq * S;
+      t.B = rhs[i]; t.ldb = ld; t.sB = dk;
+      t.C = out[i]; t.ldc = ld; t.sC = dk;
+      t.M = (int)S; t.N = (int)dk; t.K = (int)nq;
+      t.mode = q0 == 0 ? kEpiAct : kEpiAccum;
+      if (launch_gemm_ex(t, true, false, (int)H, s)) return -1;
+    }
+    GemmArgs q = wide_pv_args(nq, S, dk);
+    q.A = G; q.lda = S; q.sA = nq * S;
+    q.B = K; q.ldb = ld; q.sB = dk;
+    q.C = dQ + q0 * ld; q.ldc = ld; q.sC = dk;
+    if (launch_gemm_split(q, false, false, (int)H, gemm_split_count(q, (int)H), ws + wide_score_floats(S, H, true), s))
+      return -1;
+  }
+  return 0;
+}
 
 bool attention_in_place(int64_t D, int64_t H, int64_t ld, const void* const* ptrs, int n) {
   if (H <= 0 || D % H != 0 || ld % 4 != 0) return false;
@@ -737,6 +1071,8 @@ bool attention_in_place(int64_t D, int64_t H, int64_t ld, const void* const* ptr
 size_t attention_pad_floats(int64_t S, int64_t D, int64_t H, bool backward) {
   if (S <= 0 || H <= 0 || D % H != 0) return 0;
   const int64_t dkp = padded_dk(D / H);
+  // wide path: the score block, and in the backward its gradient
+  if (!dkp) return (size_t)wide_score_floats(S, H, backward) + wide_split_floats(S, H, D / H);
   // forward: Q K V ctx; backward: Q K V O dO dQ dK dV
   return (size_t)((backward ? 8 : 4) * S * H * dkp);
 }
@@ -783,14 +1119,12 @@ int launch_attention_fwd(const float* Q, const float* K, const float* V, float* 
     return 0;
   }
   const int64_t dkp = padded_dk(DK);
-  if (!dkp) {
-    set_error("attention: head size above 128 is not supported");
-    return -1;
-  }
   if (!pad_ws) {
-    set_error("attention: this head size or alignment needs the padding workspace");
+    set_error(dkp ? "attention: this head size or alignment needs the padding workspace"
+                  : "attention: head sizes above 128 need the score workspace");
     return -1;
   }
+  if (!dkp) return wide_fwd(Q, K, V, ctx, lse, S, H, DK, ld, scale, pad_ws, s);
   const int64_t ldp = H * dkp, n = S * ldp;
   float *Qp = pad_ws, *Kp = pad_ws + n, *Vp = pad_ws + 2 * n, *Op = pad_ws + 3 * n;
   if (pad_copy(Q, ld, Qp, S, H, DK, dkp, s) || pad_copy(K, ld, Kp, S, H, DK, dkp, s) ||
@@ -855,14 +1189,12 @@ int launch_attention_bwd(const float* Q, const float* K, const float* V, const f
   if (attention_in_place(D, H, ld, ptrs, 5))
     return flash_bwd_any(DK, Q, K, V, O, dO, lse, delta, dQ, dK, dV, S, H, ld, scale, ds, s);
   const int64_t dkp = padded_dk(DK);
-  if (!dkp) {
-    set_error("attention: head size above 128 is not supported");
-    return -1;
-  }
   if (!pad_ws) {
-    set_error("attention backward: this head size or alignment needs the padding workspace");
+    set_error(dkp ? "attention backward: this head size or alignment needs the padding workspace"
+                  : "attention backward: head sizes above 128 need the score workspace");
     return -1;
   }
+  if (!dkp) return wide_bwd(Q, K, V, dO, dQ, dK, dV, S, H, DK, ld, scale, pad_ws, s);
   const int64_t ldp = H * dkp, n = S * ldp;
   float* p[8];
   for (int i = 0; i < 8; i++) p[i] = pad_ws + i * n;

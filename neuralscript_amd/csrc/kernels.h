@@ -109,7 +109,9 @@ int launch_embedding_grad(const float* dout, const float* idx, float* dW, int64_
 // place (attention_in_place over the arrays read as float4 rows: Q, K, V,
 // and O, dO in the backward); every other head size up to 128 runs on a copy
 // padded with zero columns to the next of them, in pad_ws
-// (attention_pad_floats floats); above 128 is refused.
+// (attention_pad_floats floats).  Above 128, pad_ws (as many floats) holds
+// the scores of a block of query rows, [H][rows][S], which the GEMM kernels
+// produce and consume (rows: all S while H * S * S floats fit 1 GiB).
 bool attention_in_place(int64_t D, int64_t H, int64_t ld, const void* const* ptrs, int n);
 size_t attention_pad_floats(int64_t S, int64_t D, int64_t H, bool backward);
 int launch_attention_fwd(const float* Q, const float* K, const float* V, float* ctx, float* lse, int64_t S, int64_t D,

@@ -49,6 +49,7 @@ CASES = [
     ("dmx", 23, 115, 0, 0.0, False),
     ("smt", 33, 116, 3, 0.05, False),
     ("drp", 37, 117, 4, 0.05, False),
+    ("c5w", 400, 118, 2, 0.003, False),
 ]
 
 

@@ -33,8 +33,14 @@ def layout(name):
     return out
 
 
-def net_weights(name, seed, std=0.2):
-    return workloads.generic_weights(layout(name), shapes(name), seed, std)
+# Weight scale per network where the default would saturate the reference's
+# softmax (c5w's 320-wide layers: logits near 90, whose probabilities
+# underflow to 0 and make the reference's cross-entropy infinite).
+WEIGHT_STD = {"c5w": 0.05}
+
+
+def net_weights(name, seed, std=None):
+    return workloads.generic_weights(layout(name), shapes(name), seed, WEIGHT_STD.get(name, 0.2) if std is None else std)
 
 
 def net_weights_for(net, seed, std=0.2):

@@ -88,13 +88,44 @@ def test_attention_core_backward_matches_float64(S, D, H, store_ds):
         helpers.assert_close(got.to_host(), ref, f"attention {name} S={S} D={D} H={H} ds={store_ds}")
 
 
-@pytest.mark.parametrize("S,D,H", [(64, 320, 2), (64, 1024, 4)])
-def test_attention_head_size_above_128_is_refused(S, D, H):
-    """Head sizes above 128 have no tiled kernel: -1 and a message, before any
-    device work."""
-    Q = DA(S * D)
-    rc = runtime.lib().nsh_op_attention_fwd(Q.ptr, Q.ptr, Q.ptr, Q.ptr, None, S, D, H)
-    assert rc == -1 and "above 128" in runtime.last_error()
+# Head sizes above 128 (160, 256, 129 with rows not 16-byte aligned, 300
+# with an odd sequence length): scores materialised per block of query rows
+# and multiplied out by the GEMM kernels.  rows: query rows per block
+# (NSHIP_ATTN_WIDE_ROWS; None = the whole sequence in one block).  Score
+# rows held in registers at 4, 8 and 16 floats per thread (S up to 4096,
+# 8192, 16384 and a multiple of 4), streamed three times otherwise (S = 257,
+# 130).
+WIDE = [(64, 320, 2, None), (64, 1024, 4, None), (100, 387, 3, None), (257, 600, 2, None), (1000, 1536, 6, None),
+        (300, 512, 2, 64), (257, 600, 2, 100), (130, 320, 2, 1), (6000, 160, 1, None), (9000, 136, 1, 3000)]
+
+
+@pytest.mark.parametrize("S,D,H,rows", WIDE)
+def test_wide_head_attention_matches_float64(S, D, H, rows, monkeypatch):
+    """Forward and backward at head sizes above 128 vs float64, at the fp32
+    bar; lse as the flash kernels define it."""
+    if rows:
+        monkeypatch.setenv("NSHIP_ATTN_WIDE_ROWS", str(rows))
+    print(f"wide attention S={S} D={D} H={H} rows={rows}", flush=True)
+    Q, K, V, dO = (synth.normal(S * 30 + i, S * D, 1.0) for i in range(4))
+    gQ, gK, gV, gdO = (DA.from_host(a) for a in (Q, K, V, dO))
+    ctx, lse = DA(S * D), DA(S * H)
+    runtime.op("attention_fwd", gQ, gK, gV, ctx, lse, S, D, H)
+    helpers.assert_close(ctx.to_host(), core_ref(Q, K, V, S, D, H).ravel(), f"wide attention S={S} D={D} H={H}")
+    dk = D // H
+    Qd, Kd = Q.reshape(S, D).astype(np.float64), K.reshape(S, D).astype(np.float64)
+    lref = np.empty((H, S))
+    for h in range(H):
+        sl = slice(h * dk, (h + 1) * dk)
+        sc = Qd[:, sl] @ Kd[:, sl].T * (1.0 / np.sqrt(np.float32(dk)))
+        m = sc.max(1)
+        lref[h] = (m + np.log(np.exp(sc - m[:, None]).sum(1))) / np.log(2.0)
+    helpers.assert_close(lse.to_host(), lref.ravel(), "wide attention lse")
+    dQ_, dK_, dV_ = (DA(S * D) for _ in range(3))
+    nb = runtime.lib().nsh_op_attention_bwd_workspace(S, D, H, 1)
+    ws = DA(max(1, (nb + 3) // 4))
+    runtime.op("attention_bwd", gQ, gK, gV, ctx, gdO, lse, dQ_, dK_, dV_, S, D, H, 1, ws)
+    for name, got, ref in zip(("dQ", "dK", "dV"), (dQ_, dK_, dV_), core_bwd_ref(Q, K, V, dO, S, D, H)):
+        helpers.assert_close(got.to_host(), ref.ravel(), f"wide attention {name} S={S} D={D} H={H} rows={rows}")
 
 
 def test_attention_layer_matches_oracle():

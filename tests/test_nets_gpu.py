@@ -13,7 +13,7 @@ from neuralscript_amd import runtime, workloads
 pytestmark = pytest.mark.gpu
 
 FWD_NETS = ["c1", "c2s", "xor", "mlpt", "c3s", "c4s", "c4k", "c5t", "moet", "c5s", "moeb", "dmv", "dmw", "bop",
-            "dmx", "drp"]
+            "dmx", "drp", "c5w"]
 # outputs that are pure copies of the input (concat / slice / index / scatter):
 # bit-exact
 BITWISE = {"dmx"}

@@ -136,7 +136,7 @@ def test_100_step_loss_curve_matches_reference(curve):
 
 @pytest.mark.parametrize("name,rows", [("c5t", 40), ("mlpt", 17), ("c5s", 64), ("c5s", 2048), ("c5h", 192),
                                        ("c5h", 100), ("moet", 41), ("moet", 300), ("moeb", 4096),
-                                       ("smt", 64), ("drp", 64), ("drp", 29)])
+                                       ("smt", 64), ("drp", 64), ("drp", 29), ("c5w", 400), ("c5w", 130)])
 def test_every_value_of_one_train_step_matches_oracle(name, rows):
     """Each intermediate and gradient of one training step (read back from
     the device by IR value name) against the oracle's value of the same
