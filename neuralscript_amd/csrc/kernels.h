@@ -194,7 +194,7 @@ struct MoeWork {
   int* seg;        // [E + 1] segment starts of the expert-sorted order
   int* perm;       // [M]     expert-sorted position -> token
   int* tiles;      // [2 * (M/128 + E)] (expert, m-tile) pairs
-  int* ntiles;     // [1]
+  int* ntiles;     // [1]; above 4096 experts the dispatch scan's tables (3E+2 ints) follow it
   float* hidden;   // [M, H]  GELU(x We1[e]) in expert-sorted order
   float* pre;      // [M, H]  x We1[e] before GELU (training only, else null)
 };

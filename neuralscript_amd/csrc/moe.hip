@@ -33,9 +33,10 @@ namespace {
 constexpr int kTok = 64;   // tokens per router workgroup
 constexpr int kKS = 32;    // k slab
 constexpr int kBlk = 256;  // tokens per dispatch block
-// Experts of one MoE layer: the scan's per-expert tables (3 E + 2 ints) sit
-// in 64 KB of dynamic LDS.
-constexpr int kMaxExperts = 4096;
+// Experts whose scan tables (3 E + 2 ints) sit in 64 KB of dynamic LDS;
+// beyond, the tables live in the ints workspace (moe_work_ints reserves
+// them after ntiles).
+constexpr int kLdsExperts = 4096;
 
 // exp(x) correctly rounded to float (double evaluation, one rounding).
 __device__ __forceinline__ float exp_rn(float x) { return (float)exp((double)x); }
@@ -410,13 +411,14 @@ __global__ __launch_bounds__(256) void moe_scan_lds_kernel(int* __restrict__ bco
 
 // Expert segments, per-block offsets (in place over bcount) and the
 // (expert, m-tile) list.  One workgroup; thread t owns experts t, t + 256,
-// ...; the per-expert tables live in dynamic LDS (3 E + 2 ints).
+// ...; the per-expert tables (3 E + 2 ints) live in dynamic LDS, or in gtab
+// (global memory) above kLdsExperts.
 __global__ __launch_bounds__(256) void moe_scan_kernel(int* __restrict__ bcount, int* __restrict__ seg,
                                                        int* __restrict__ tiles, int* __restrict__ ntiles, int nblk,
-                                                       int E, int bm) {
+                                                       int E, int bm, int* __restrict__ gtab) {
   extern __shared__ int scan_tab[];
-  int* tot = scan_tab;
-  int* base = scan_tab + E;
+  int* tot = gtab ? gtab : scan_tab;  // gtab: the tables in global memory (E > kLdsExperts)
+  int* base = tot + E;
   int* tb = base + E + 1;
   const int t = threadIdx.x;
   for (int e = t; e < E; e += 256) {
@@ -480,15 +482,17 @@ __global__ void zero_rows_kernel(const int* __restrict__ best, float* __restrict
 
 size_t moe_work_ints(int64_t M, int64_t E) {
   const int64_t nblk = ceil_div(M, kBlk);
-  // best, rank, perm: 3M; bcount: nblk*E; seg: E+1; tiles: 2*(M/128+E+1); ntiles: 1
-  return (size_t)(3 * M + nblk * E + (E + 1) + 2 * (ceil_div(M, 128) + E + 1) + 1);
+  // best, rank, perm: 3M; bcount: nblk*E; seg: E+1; tiles: 2*(M/128+E+1); ntiles: 1;
+  // above kLdsExperts the scan's tables: 3E+2
+  return (size_t)(3 * M + nblk * E + (E + 1) + 2 * (ceil_div(M, 128) + E + 1) + 1 +
+                  (E > kLdsExperts ? 3 * E + 2 : 0));
 }
 
 int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, const MoeWork& w, int64_t M, int64_t D,
                      int64_t E, hipStream_t s) {
   if (M <= 0) return 0;
-  if (E > kMaxExperts || M > INT32_MAX / 2) {
-    set_error("moe: more than " + std::to_string(kMaxExperts) + " experts or too many tokens");
+  if (M > INT32_MAX / 2 || E > INT32_MAX / 4 || (int64_t)ceil_div(M, kBlk) * E > INT32_MAX) {
+    set_error("moe: too many tokens or experts");
     return -1;
   }
   const int m = (int)M, d = (int)D, e = (int)E;
@@ -525,9 +529,12 @@ int launch_moe_route(const float* x, const float* Wg, const uint8_t* active, con
   NSH_LAUNCHED();
   if ((int64_t)nblk * E <= kScanLds && E <= 256)
     hipLaunchKernelGGL(moe_scan_lds_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128);
-  else
+  else if (E <= kLdsExperts)
     hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), (3 * E + 2) * sizeof(int), s, w.bcount, w.seg, w.tiles,
-                       w.ntiles, nblk, e, 128);
+                       w.ntiles, nblk, e, 128, nullptr);
+  else
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(256), 0, s, w.bcount, w.seg, w.tiles, w.ntiles, nblk, e, 128,
+                       w.ntiles + 1);
   NSH_LAUNCHED();
   hipLaunchKernelGGL(moe_place_kernel, dim3(nblk), dim3(kBlk), 0, s, w.best, w.rank, w.bcount, w.perm, m, e);
   NSH_LAUNCHED();

@@ -70,7 +70,7 @@ def test_moe_lifecycle_matches_reference_fixture():
 @pytest.mark.parametrize("M,D,E,H,mask", [(1000, 64, 8, 96, None), (3000, 128, 64, 64, None),
                                           (777, 64, 16, 32, "some"), (513, 32, 130, 16, None),
                                           (600, 32, 256, 16, "some"), (400, 32, 300, 8, "some"),
-                                          (300, 16, 1000, 4, None)])
+                                          (300, 16, 1000, 4, None), (700, 16, 5000, 2, "some")])
 def test_moe_routing_is_bit_exact(M, D, E, H, mask):
     print(f"moe routing M={M} D={D} E={E} H={H}", flush=True)
     ir = ("ns.func @MOE {\n"
@@ -343,13 +343,14 @@ def test_moe_backward_at_production_shape():
     assert not bad, bad
 
 
-@pytest.mark.parametrize("E,rows", [(300, 300), (1000, 257)])
+@pytest.mark.parametrize("E,rows", [(300, 300), (1000, 257), (6000, 700)])
 def test_moe_training_step_with_many_experts(E, rows):
     """More than 256 experts (the router's logits by expert tiles, routing
-    from them, the dispatch scan's tables in dynamic LDS, the backward's
-    routing probabilities per lane): moet's network with E experts (three
-    quarters live), one training step against the oracle -- expert choices
-    bit-exact, every MoE gradient and the loss at the fp32 bar."""
+    from them, the dispatch scan's tables in dynamic LDS -- in the ints
+    workspace above 4096 experts --, the backward's routing probabilities
+    per lane): moet's network with E experts (three quarters live), one
+    training step against the oracle -- expert choices bit-exact, every MoE
+    gradient and the loss at the fp32 bar."""
     print(f"moe training E={E} rows={rows}", flush=True)
     ir = (helpers.ir_text("moet").replace("Tensor[32, 8]", f"Tensor[32, {E}]")
           .replace("Tensor[8, 1536]", f"Tensor[{E}, 1536]").replace("experts=8", f"experts={E}")
