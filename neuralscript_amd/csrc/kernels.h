@@ -136,8 +136,10 @@ struct MuonMat {
   float* w;          // weight [r][c], updated in place
   const float* g;    // gradient [r][c]
   float* T;          // work: vectors contiguous, [C][R]; q vectors on exit
-  float* red;        // sliced path (R > 8192): [2][C][slices] partial sums, mgs_red_floats(R, C); else unused
+  float* red;        // mgs_red_floats(R, C): sliced path (R > 8192) partial sums; panel path (R > 512) the
+                     // row-compaction tables; null when that is 0
   int R, C;          // vector length, number of vectors
+  int ldT;           // stride of T's vectors: R (MGS may run on fewer, compacted rows, R set meanwhile)
   int transposed;    // r < c: the vectors are the rows of g
   float le, decay;   // lr * sqrt(min(r, c)), 0.01 * lr
 };
@@ -147,6 +149,10 @@ int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipSt
 // Longest vector the register-panel MGS takes; longer ones go through the
 // sliced path (and need MuonMat::red).
 int64_t mgs_max_panel_len();
+// Whether a register-panel matrix (R <= mgs_max_panel_len()) whose vectors
+// have at most live_bound nonzero elements could run MGS on compacted rows
+// (a smaller register layout); its MuonMat::red (mgs_red_floats) enables it.
+bool mgs_rows_may_compact(int64_t R, int64_t live_bound);
 // A second stream for the sliced-path launches of launch_mgs, and the two
 // events (no timing) that fork it from and join it back to the main stream.
 struct MgsSide {

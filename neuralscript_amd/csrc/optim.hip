@@ -634,12 +634,12 @@ __device__ __forceinline__ void row_store(gfloat* __restrict__ row, int R, int t
 // vectors held in x, in order; q_{jj+1} and q_{jj+2} are in flight while
 // q_jj's projections reduce.
 template <int EPT, bool VEC, int NV>
-__device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R, int q0, float (&x)[NV][EPT],
-                                            float (*red)[64 * kPB], int& par) {
+__device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R, int ld, int q0,
+                                            float (&x)[NV][EPT], float (*red)[64 * kPB], int& par) {
   const int t = threadIdx.x;
   float qn[EPT], qn2[EPT];
-  row_load<EPT, VEC>(T + (int64_t)q0 * R, R, t, true, qn);
-  row_load<EPT, VEC>(T + (int64_t)(q0 + 1) * R, R, t, true, qn2);
+  row_load<EPT, VEC>(T + (int64_t)q0 * ld, R, t, true, qn);
+  row_load<EPT, VEC>(T + (int64_t)(q0 + 1) * ld, R, t, true, qn2);
 #pragma unroll 1
   for (int jj = 0; jj < kPB; jj++) {
     float qv[EPT];
@@ -648,7 +648,7 @@ __device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R,
       qv[e] = qn[e];
       qn[e] = qn2[e];
     }
-    row_load<EPT, VEC>(T + (int64_t)(q0 + jj + 2) * R, R, t, jj + 2 < kPB, qn2);
+    row_load<EPT, VEC>(T + (int64_t)(q0 + jj + 2) * ld, R, t, jj + 2 < kPB, qn2);
     float d[NV];
 #pragma unroll
     for (int v = 0; v < NV; v++) {
@@ -671,7 +671,7 @@ __device__ __forceinline__ void mgs_project(const gfloat* __restrict__ T, int R,
 // soon as it is final, so the stores drain while the later steps run.
 template <int EPT, bool VEC>
 __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (*red)[64 * kPB], int& par,
-                                           gfloat* __restrict__ T, int R, int c0) {
+                                           gfloat* __restrict__ T, int R, int ld, int c0) {
 #pragma unroll
   for (int jj = 0; jj < kPB; jj++) {
     if (jj >= nv) break;
@@ -683,7 +683,7 @@ __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (
     const float nrm = sqrtf(s[0]) + 1e-30f, rn = 1.f / nrm;
 #pragma unroll
     for (int e = 0; e < EPT; e++) x[jj][e] = div_shared(x[jj][e], nrm, rn);
-    row_store<EPT, VEC>(T + (int64_t)(c0 + jj) * R, R, threadIdx.x, x[jj]);
+    row_store<EPT, VEC>(T + (int64_t)(c0 + jj) * ld, R, threadIdx.x, x[jj]);
     if (jj + 1 >= nv) break;
     float d[kPB];
 #pragma unroll
@@ -706,7 +706,7 @@ __device__ __forceinline__ void mgs_factor(float (&x)[kPB][EPT], int nv, float (
 }
 
 // Elements per thread for a vector of length R (R <= kMaxPanelR).
-__device__ __forceinline__ int panel_ept(int R) {
+__host__ __device__ __forceinline__ int panel_ept(int R) {
   return R <= kPanelThreads ? 1 : R <= 2 * kPanelThreads ? 2 : R <= 4 * kPanelThreads ? 4
          : R <= 8 * kPanelThreads ? 8 : 16;
 }
@@ -715,7 +715,8 @@ __device__ __forceinline__ int panel_ept(int R) {
 // for matrix M's vector length and alignment.
 #define NSH_WITH_LAYOUT(M, CALL)                                                             \
   do {                                                                                       \
-    const bool vec_ = (M).R % 4 == 0 && (reinterpret_cast<uintptr_t>((M).T) & 15) == 0;     \
+    const bool vec_ = (M).R % 4 == 0 && (M).ldT % 4 == 0 &&                                   \
+                      (reinterpret_cast<uintptr_t>((M).T) & 15) == 0;                          \
     switch (panel_ept((M).R)) {                                                              \
       case 1: { constexpr int E = 1; constexpr bool V = false; CALL; } break;               \
       case 2: { constexpr int E = 2; constexpr bool V = false; CALL; } break;               \
@@ -738,21 +739,21 @@ __device__ __forceinline__ int panel_ept(int R) {
 // nv vectors c0 ..., and, for the lead workgroup (whose vectors are panel
 // jp + 1), factorize them.
 template <int EPT, bool VEC>
-__device__ __forceinline__ void mgs_panel_body(gfloat* __restrict__ T, int R, int jp, int c0, int nv, bool lead,
-                                               float (*red)[64 * kPB]) {
+__device__ __forceinline__ void mgs_panel_body(gfloat* __restrict__ T, int R, int ld, int jp, int c0, int nv,
+                                               bool lead, float (*red)[64 * kPB]) {
   const int t = threadIdx.x;
   float x[kPB][EPT];
 #pragma unroll
-  for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, v < nv, x[v]);
+  for (int v = 0; v < kPB; v++) row_load<EPT, VEC>(T + (int64_t)(c0 + v) * ld, R, t, v < nv, x[v]);
   int par = 0;
-  if (jp >= 0) mgs_project<EPT, VEC, kPB>(T, R, jp, x, red, par);
+  if (jp >= 0) mgs_project<EPT, VEC, kPB>(T, R, ld, jp, x, red, par);
   if (lead) {
-    mgs_factor<EPT, VEC>(x, nv, red, par, T, R, c0);
+    mgs_factor<EPT, VEC>(x, nv, red, par, T, R, ld, c0);
     return;
   }
 #pragma unroll
   for (int v = 0; v < kPB; v++)
-    if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * R, R, t, x[v]);
+    if (v < nv) row_store<EPT, VEC>(T + (int64_t)(c0 + v) * ld, R, t, x[v]);
 }
 
 // Launch for panel jp (jp < 0: the first launch, no projections): vectors
@@ -774,7 +775,150 @@ __global__ __launch_bounds__(kPanelThreads) void mgs_panel_kernel(const MuonMat*
   const int nv = min(kPB, M.C - c0);
   gfloat* T = as_global(M.T);
   const int R = M.R;
-  NSH_WITH_LAYOUT(M, (mgs_panel_body<E, V>(T, R, jp, c0, nv, b == 0, red)));
+  const int ld = M.ldT;
+  NSH_WITH_LAYOUT(M, (mgs_panel_body<E, V>(T, R, ld, jp, c0, nv, b == 0, red)));
+}
+
+// ---- zero rows of the panel path ----------------------------------------------
+// Element k of every vector is zero when row k of the gradient is (an
+// embedding row that no token of the step used), and stays zero through
+// MGS: q_j[k] = v_j[k] / |v_j| = 0 and every projection subtracts d * 0 from
+// it.  When dropping those rows moves the vectors into a smaller register
+// layout (panel_ept), each vector is compacted in place to its live rows
+// (padded with zeros to a multiple of 4; the stride ldT stays), MGS runs
+// with R set to that length, and the q vectors are scattered back with
+// zeros in the dropped rows.  Only the order in which the block sums add
+// the elements changes.  MuonMat::red of a panel matrix (R > 512) holds, as
+// ints: [0] the compacted length (0: not compacted), [1] the live rows,
+// then rank[ldT] (flag, then compacted index or -1) and rows[ldT] (row of
+// each compacted index).
+constexpr int kRowHdr = 2;
+__device__ __forceinline__ bool rows_compactable(const MuonMat& M) {
+  return M.red && M.ldT <= kMaxPanelR && M.ldT > kPanelThreads;
+}
+
+// rank[k] = 1 if row k is nonzero in some vector, else 0: 64 rows x 16
+// groups of vectors per 1024-thread workgroup; blockIdx.y = matrix.
+__global__ __launch_bounds__(1024) void mgs_rows_live_kernel(const MuonMat* __restrict__ mats, int nmat) {
+  __shared__ int any[16][64];
+  const MuonMat& M = mats[blockIdx.y];
+  if (!rows_compactable(M)) return;
+  const int ld = M.ldT, C = M.C;
+  const int k = blockIdx.x * 64 + (threadIdx.x & 63), grp = threadIdx.x >> 6;
+  if (blockIdx.x * 64 >= ld) return;
+  const gfloat* __restrict__ T = as_global(M.T);
+  bool nz = false;
+  if (k < ld) {
+    int c = grp;
+    for (; c + 16 * 7 < C; c += 16 * 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = T[(int64_t)(c + 16 * u) * ld + k];
+#pragma unroll
+      for (int u = 0; u < 8; u++) nz |= v[u] != 0.f;
+    }
+    for (; c < C; c += 16) nz |= T[(int64_t)c * ld + k] != 0.f;
+  }
+  any[grp][threadIdx.x & 63] = nz;
+  __syncthreads();
+  if (grp == 0 && k < ld) {
+    int a = 0;
+#pragma unroll
+    for (int g = 0; g < 16; g++) a |= any[g][threadIdx.x];
+    reinterpret_cast<int*>(M.red)[kRowHdr + k] = a;
+  }
+  (void)nmat;
+}
+
+// Per matrix (blockIdx.x), one workgroup: the live rows' compacted indices
+// (a prefix sum over the flags), the compacted length, and whether to
+// compact; if so, the matrix's R becomes that length until
+// mgs_rows_scatter_kernel restores it.
+__global__ __launch_bounds__(1024) void mgs_rows_plan_kernel(MuonMat* __restrict__ mats, int nmat) {
+  __shared__ int wsum[16];
+  MuonMat& M = mats[blockIdx.x];
+  if (!rows_compactable(M)) return;
+  int* __restrict__ hdr = reinterpret_cast<int*>(M.red);
+  int* __restrict__ rank = hdr + kRowHdr;
+  int* __restrict__ rows = rank + M.ldT;
+  const int ld = M.ldT, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  constexpr int kPer = kMaxPanelR / 1024;  // rows per thread, contiguous
+  int f[kPer], cnt = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int k = t * kPer + i;
+    f[i] = k < ld ? rank[k] : 0;
+    cnt += f[i];
+  }
+  int incl = cnt;  // inclusive prefix over the wave, then over the waves
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int off = incl - cnt;
+  for (int i = 0; i < w; i++) off += wsum[i];
+  int total = 0;
+  for (int i = 0; i < 16; i++) total += wsum[i];
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int k = t * kPer + i;
+    if (k < ld) {
+      rank[k] = f[i] ? off : -1;
+      if (f[i]) rows[off++] = k;
+    }
+  }
+  const int rc = (total + 3) & ~3;
+  // worth it only when the vectors move into a smaller register layout
+  // (an all-zero matrix is left as it is: its q vectors are zero either way)
+  const bool compact = total > 0 && panel_ept(rc) < panel_ept(ld);
+  if (t == 0) {
+    hdr[0] = compact ? rc : 0;
+    hdr[1] = total;
+    if (compact) M.R = rc;
+  }
+  (void)nmat;
+}
+
+// Vector c = blockIdx.x of matrix blockIdx.y through LDS: its live rows to
+// the front (then zeros up to the compacted length), or back.
+constexpr int kRowVecThreads = 512;
+__global__ __launch_bounds__(kRowVecThreads) void mgs_rows_compact_kernel(const MuonMat* __restrict__ mats, int nmat) {
+  __shared__ float v[kMaxPanelR];
+  const MuonMat& M = mats[blockIdx.y];
+  if (!rows_compactable(M) || (int)blockIdx.x >= M.C) return;
+  const int* __restrict__ hdr = reinterpret_cast<const int*>(M.red);
+  const int rc = hdr[0], live = hdr[1];
+  if (rc == 0) return;
+  const int* __restrict__ rows = hdr + kRowHdr + M.ldT;
+  const int ld = M.ldT;
+  gfloat* __restrict__ x = as_global(M.T) + (int64_t)blockIdx.x * ld;
+  for (int k = threadIdx.x; k < ld; k += kRowVecThreads) v[k] = x[k];
+  __syncthreads();
+  for (int i = threadIdx.x; i < rc; i += kRowVecThreads) x[i] = i < live ? v[rows[i]] : 0.f;
+  (void)nmat;
+}
+
+__global__ __launch_bounds__(kRowVecThreads) void mgs_rows_scatter_kernel(MuonMat* __restrict__ mats, int nmat) {
+  __shared__ float v[kMaxPanelR / 2];
+  MuonMat& M = mats[blockIdx.y];
+  if (!rows_compactable(M) || (int)blockIdx.x >= M.C) return;
+  const int* __restrict__ hdr = reinterpret_cast<const int*>(M.red);
+  const int rc = hdr[0];
+  if (rc == 0) return;
+  const int* __restrict__ rank = hdr + kRowHdr;
+  const int ld = M.ldT;
+  gfloat* __restrict__ x = as_global(M.T) + (int64_t)blockIdx.x * ld;
+  for (int i = threadIdx.x; i < rc; i += kRowVecThreads) v[i] = x[i];
+  __syncthreads();
+  for (int k = threadIdx.x; k < ld; k += kRowVecThreads) {
+    const int r = rank[k];
+    x[k] = r >= 0 ? v[r] : 0.f;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) M.R = ld;
+  (void)nmat;
 }
 
 // w -= le * q + (0.01 lr) * w, q = T (normalised vectors): element [k][j]
@@ -879,7 +1023,14 @@ int launch_adamw(float* w, const float* g, float* m, float* v, int64_t n, float 
 
 int64_t mgs_max_panel_len() { return kMaxPanelR; }
 
+bool mgs_rows_may_compact(int64_t R, int64_t live_bound) {
+  if (R > kMaxPanelR || R <= kPanelThreads || live_bound <= 0) return false;
+  return panel_ept((int)((std::min(R, live_bound) + 3) & ~3)) < panel_ept((int)R);
+}
+
 size_t mgs_red_floats(int64_t R, int64_t C) {
+  // panel path: the row-compaction tables (header, rank, rows; ints)
+  if (R <= kMaxPanelR) return R > kPanelThreads ? (size_t)(kRowHdr + 2 * R) : 0;
   // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl], their
   // totals [kSlicePanel][C], and each slice's count of vectors up to its
   // last nonzero one [nsl] (ints)
@@ -917,6 +1068,25 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
   // stream given, the sliced launches (bound by HBM) run on the side stream
   // beside the panel launches (bound by one workgroup's chain), forked from
   // and joined back to s by events.
+  // panel-path matrices whose zero rows may be dropped (mgs_rows_*)
+  int rows_r = 0, rows_c = 0;
+  for (int i = 0; i < nmat; i++) {
+    const MuonMat& M = h_mats[i];
+    if (M.red && M.R <= kMaxPanelR && M.R > kPanelThreads) {
+      rows_r = std::max(rows_r, M.R);
+      rows_c = std::max(rows_c, M.C);
+    }
+  }
+  MuonMat* dm = const_cast<MuonMat*>(d_mats);
+  if (rows_r > 0) {
+    hipLaunchKernelGGL(mgs_rows_live_kernel, dim3((unsigned)ceil_div(rows_r, 64), nmat), dim3(1024), 0, s, d_mats,
+                       nmat);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(mgs_rows_plan_kernel, dim3(nmat), dim3(1024), 0, s, dm, nmat);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(mgs_rows_compact_kernel, dim3(rows_c, nmat), dim3(kRowVecThreads), 0, s, d_mats, nmat);
+    NSH_LAUNCHED();
+  }
   const bool fork = side && side->stream && slices > 0 && max_c > 0;
   hipStream_t ss = fork ? side->stream : s;
   if (fork) {
@@ -959,6 +1129,10 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
     NSH_LAUNCHED();
   }
   if (fork) NSH_CHECK(hipStreamWaitEvent(s, side->join, 0));
+  if (rows_r > 0) {
+    hipLaunchKernelGGL(mgs_rows_scatter_kernel, dim3(rows_c, nmat), dim3(kRowVecThreads), 0, s, dm, nmat);
+    NSH_LAUNCHED();
+  }
   return 0;
 }
 

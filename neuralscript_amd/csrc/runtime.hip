@@ -201,6 +201,9 @@ struct Frame {
   float* direct = nullptr;
   const float* direct_in = nullptr;
   size_t direct_in_n = 0;
+  // embedding weight gradients (by value id) and their token counts: at most
+  // that many of their rows are nonzero
+  std::map<int, int64_t> emb_tokens;
 };
 
 float* scratch(ns_model* m, const std::string& key, size_t n) {
@@ -756,8 +759,13 @@ int optimizer_step(ns_model* m, Frame& fr, const Instr& I, float lr) {
       mm.transposed = r < c ? 1 : 0;
       mm.R = (int)(r < c ? c : r);
       mm.C = (int)(r < c ? r : c);
+      mm.ldT = mm.R;
       mm.T = scratch(m, "muonT" + std::to_string(wid), (size_t)n);
-      const size_t nred = mgs_red_floats(mm.R, mm.C);
+      // the panel path's row compaction only where it can pay: an embedding
+      // gradient with fewer live rows than its vector length's layout needs
+      const auto et = fr.emb_tokens.find(gid);
+      const bool rows = !mm.transposed && et != fr.emb_tokens.end() && mgs_rows_may_compact(mm.R, et->second);
+      const size_t nred = mm.R > mgs_max_panel_len() || rows ? mgs_red_floats(mm.R, mm.C) : 0;
       mm.red = nred ? scratch(m, "muonP" + std::to_string(wid), nred) : nullptr;
       if (!mm.T || (nred && !mm.red)) return -1;
       mm.le = lr * sqrtf((float)std::min(r, c));
@@ -1021,6 +1029,7 @@ int run_train(ns_model* m, const float* d_x, size_t n_in, const float* d_y, floa
             Prof p(m, "embedding_grad");
             if (launch_embedding_grad(fr.ptr[I.in[0]], fr.ptr[I.in[1]], dW, n, W.rows, W.cols, ws, s) != 0)
               return -1;
+            fr.emb_tokens[I.res] = n;
             break;
           }
           case Op::AttnGradX: case Op::AttnGradWq: case Op::AttnGradWk: case Op::AttnGradWv: case Op::AttnGradWo: {
@@ -1885,6 +1894,7 @@ static int op_muon(float* w, const float* g, int64_t r, int64_t c, float le, flo
   mm.transposed = r < c ? 1 : 0;
   mm.R = (int)(r < c ? c : r);
   mm.C = (int)(r < c ? r : c);
+  mm.ldT = mm.R;
   char* base = (char*)ws;
   mm.T = (float*)(base + 256);
   mm.red = mgs_red_floats(mm.R, mm.C) ? mm.T + r * c : nullptr;
@@ -1917,6 +1927,7 @@ int nsh_op_muon_multi(int n, float* const* w, const float* const* g, const int64
     mm.transposed = r[i] < c[i] ? 1 : 0;
     mm.R = (int)(r[i] < c[i] ? c[i] : r[i]);
     mm.C = (int)(r[i] < c[i] ? r[i] : c[i]);
+    mm.ldT = mm.R;
     mm.T = wsf;
     wsf += r[i] * c[i];
     const size_t nred = mgs_red_floats(mm.R, mm.C);

@@ -51,6 +51,42 @@ def test_orthonormalize_matches_oracle_mgs(r, c):
     helpers.assert_close(got, ref, f"mgs {r}x{c}")
 
 
+# Gradients whose rows are zero in every vector (an embedding's unused
+# vocabulary rows).  Compacted to the live rows when that moves the vectors
+# into a smaller register layout: 8192 -> ~3300 (16 -> 8 elements a thread),
+# 2048 -> ~410 (4 -> 1), odd 5001 -> ~2500 (scalar rows, 16 -> 8), and the
+# transposed case (zero columns of a [64, 8192] gradient); left as they are
+# otherwise: 30% zero rows of 8192 (still 16 a thread), an all-zero matrix.
+@pytest.mark.parametrize("r,c,frac", [(8192, 64, 0.6), (64, 8192, 0.6), (2048, 100, 0.8), (5001, 24, 0.5),
+                                      (8192, 40, 0.3), (4096, 16, 1.0)])
+def test_orthonormalize_with_zero_rows(r, c, frac):
+    """Q against the oracle at the fp32 bar, exactly zero in the zero rows;
+    then the whole Muon step (the weight decay still applies to those
+    rows)."""
+    print(f"mgs zero rows {r}x{c} frac={frac}", flush=True)
+    g = synth.normal(r + 3 * c, r * c).reshape(r, c)
+    rng = np.random.default_rng(r + c)
+    if r >= c:
+        dead = rng.random(r) < frac
+        g[dead, :] = 0.0
+    else:
+        dead = rng.random(c) < frac
+        g[:, dead] = 0.0
+    g = g.ravel()
+    q = DA(r * c)
+    runtime.op("orthonormalize", DA.from_host(g), q, r, c, ws(r, c))
+    got = q.to_host()
+    helpers.assert_close(got, oracle.orthonom(g, r, c), f"mgs {r}x{c} with zero rows")
+    G = got.reshape(r, c)
+    assert not np.any(G[dead, :] if r >= c else G[:, dead])
+    w = synth.normal(5, r * c, 0.2)
+    dw, dg, dws = DA.from_host(w), DA.from_host(g), ws(r, c)  # buffers live across the call
+    runtime.lib().nsh_op_muon_step(dw.ptr, dg.ptr, r, c, ctypes.c_float(0.02), dws.ptr)
+    ref = w.copy()
+    oracle.lib().or_muon_step(oracle.fp(ref), oracle.fp(g.copy()), r, c, ctypes.c_float(0.02))
+    helpers.assert_close(dw.to_host(), ref, f"muon step {r}x{c} with zero rows")
+
+
 def shifted(a, off):
     """A device copy of `a` starting `off` floats into its buffer (off = 1
     leaves the data 4 bytes past a 16-byte boundary)."""
