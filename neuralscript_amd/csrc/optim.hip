@@ -231,20 +231,26 @@ __device__ __forceinline__ bool slice_of(const MuonMat* __restrict__ mats, int n
 
 // A thread's share of one slice of the vectors T[c][0..R): kSliceEPT
 // elements, float4 groups when the rows allow (R % 4 == 0, 16-byte aligned).
+// Vector c is T's vector lv[c] when a list lv is given (the nonzero
+// vectors, in order), else vector c itself.
 struct SliceIO {
   gfloat* __restrict__ T;
   int R;
   bool vec;
   int64_t s0;
   int t;
-  __device__ SliceIO(const MuonMat& M, int b)
+  const int* __restrict__ lv;
+  __device__ SliceIO(const MuonMat& M, int b, const int* list = nullptr)
       : T(as_global(M.T)), R(M.R), vec(M.R % 4 == 0 && (reinterpret_cast<uintptr_t>(M.T) & 15) == 0),
-        s0((int64_t)b * kSliceLen), t(threadIdx.x) {}
+        s0((int64_t)b * kSliceLen), t(threadIdx.x), lv(list) {}
   __device__ int64_t at(int e) const {
     return vec ? s0 + 4 * (t + kSliceThreads * (e >> 2)) + (e & 3) : s0 + t + kSliceThreads * e;
   }
+  __device__ int64_t base(int c) const {
+    return (int64_t)(lv ? __builtin_amdgcn_readfirstlane(lv[c]) : c) * R;  // c is the same in every lane
+  }
   __device__ void load(int c, float (&x)[kSliceEPT]) const {
-    const gfloat* row = T + (int64_t)c * R;
+    const gfloat* row = T + base(c);
     if (vec) {
 #pragma unroll
       for (int i = 0; i < kSliceEPT / 4; i++) {
@@ -259,7 +265,7 @@ struct SliceIO {
     }
   }
   __device__ void store(int c, const float (&x)[kSliceEPT]) const {
-    gfloat* row = T + (int64_t)c * R;
+    gfloat* row = T + base(c);
     if (vec) {
 #pragma unroll
       for (int i = 0; i < kSliceEPT / 4; i++) {
@@ -281,56 +287,103 @@ __device__ __forceinline__ float* slice_dots(const MuonMat& M) { return M.red + 
 __device__ __forceinline__ float* slice_dot_totals(const MuonMat& M) {
   return slice_dots(M) + (size_t)kSlicePanel * M.C * mgs_slices(M.R);
 }
-__device__ __forceinline__ int* slice_live(const MuonMat& M) {
-  return reinterpret_cast<int*>(slice_dot_totals(M) + (size_t)kSlicePanel * M.C);
+// Then the vectors' liveness: per slice a bit mask of the vectors nonzero
+// in it [nsl][ceil(C / 32)], the number of nonzero vectors, and their list.
+__device__ __forceinline__ int slice_words(const MuonMat& M) { return (M.C + 31) >> 5; }
+__device__ __forceinline__ unsigned* slice_masks(const MuonMat& M) {
+  return reinterpret_cast<unsigned*>(slice_dot_totals(M) + (size_t)kSlicePanel * M.C);
 }
-
-// Vectors past the last nonzero one (c >= the returned count) are exactly
-// zero, and stay so: every projection onto them and of them is 0 * q, and
-// each normalises to 0 / (0 + 1e-30) = 0 -- they need no work at all, and
-// the others' results do not depend on them (a gradient of MoE expert
-// weights holds zero rows for the experts without tokens).  The count is
-// the maximum over the slices' counts (mgs_slice_live_kernel), the same in
-// every workgroup.
-__device__ __forceinline__ int slice_live_count(const MuonMat& M) {
-  const int* __restrict__ lv = slice_live(M);
-  const int nsl = mgs_slices(M.R);
-  int m = 0;
-  for (int i = threadIdx.x & 63; i < nsl; i += 64) m = max(m, lv[i]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = max(m, __shfl_xor(m, o));
-  return m;
+__device__ __forceinline__ int* slice_nlive(const MuonMat& M) {
+  return reinterpret_cast<int*>(slice_masks(M) + (size_t)mgs_slices(M.R) * slice_words(M));
 }
+__device__ __forceinline__ const int* slice_list(const MuonMat& M) { return slice_nlive(M) + 1; }
 
-// Each slice's count of vectors up to its last nonzero one, from the last
-// vector down (a slice stops at its first nonzero element).
-__global__ __launch_bounds__(kSliceThreads) void mgs_slice_live_kernel(const MuonMat* __restrict__ mats, int nmat);
-
+// A zero vector stays zero and changes no other: every projection onto it
+// and of it is 0 * q, and it normalises to 0 / (0 + 1e-30) = 0 (a gradient
+// of MoE expert weights holds zero rows for the experts without tokens).
+// The sliced launches therefore run over the nonzero vectors only, in
+// order (c indexes that list, slice_list), and leave the zero ones as they
+// are.  First each slice's mask of the vectors nonzero in it, 32 vectors a
+// word: a thread's elements of 8 vectors in flight, the bits OR-reduced
+// over the workgroup.
 __global__ __launch_bounds__(kSliceThreads) void mgs_slice_live_kernel(const MuonMat* __restrict__ mats, int nmat) {
-  __shared__ int any[4];
+  __shared__ unsigned wbits[4];
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
   const SliceIO io(M, b);
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  int n = 0;
-  for (int c = M.C - 1; c >= 0; c--) {
-    float x[kSliceEPT];
-    io.load(c, x);
-    bool nz = false;
+  const int t = threadIdx.x, w = t >> 6, C = M.C, W = slice_words(M);
+  unsigned* __restrict__ out = slice_masks(M) + (size_t)b * W;
+  for (int wd = 0; wd < W; wd++) {
+    unsigned bits = 0u;
+    for (int i0 = 0; i0 < 32; i0 += 8) {
+      float x[8][kSliceEPT];
 #pragma unroll
-    for (int e = 0; e < kSliceEPT; e++) nz |= x[e] != 0.f;
-    const bool wnz = __ballot(nz) != 0;
-    if (lane == 0) any[w] = wnz;
+      for (int u = 0; u < 8; u++) {
+        const int c = 32 * wd + i0 + u;
+        if (c < C) io.load(c, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = 32 * wd + i0 + u;
+        bool nz = false;
+#pragma unroll
+        for (int e = 0; e < kSliceEPT; e++) nz |= x[u][e] != 0.f;
+        if (c < C && nz) bits |= 1u << (i0 + u);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) bits |= (unsigned)__shfl_xor((int)bits, o, 64);
+    __syncthreads();  // the previous word's readers are done
+    if ((t & 63) == 0) wbits[w] = bits;
     __syncthreads();
-    const bool found = any[0] | any[1] | any[2] | any[3];
-    __syncthreads();
-    if (found) {
-      n = c + 1;
-      break;
+    if (t == 0) out[wd] = wbits[0] | wbits[1] | wbits[2] | wbits[3];
+  }
+}
+
+// Per long matrix (blockIdx.x), one workgroup: the masks OR-ed over the
+// slices, then the nonzero vectors' list in ascending order and its length
+// (every vector when the words do not fit the workgroup's table).
+constexpr int kLiveWords = 2048;
+__global__ __launch_bounds__(256) void mgs_slice_list_kernel(const MuonMat* __restrict__ mats, int nmat) {
+  __shared__ unsigned words[kLiveWords];
+  __shared__ int offs[kLiveWords];
+  const MuonMat& M = mats[blockIdx.x];
+  if (M.R <= kMaxPanelR) return;
+  const int t = threadIdx.x, C = M.C, W = slice_words(M), nsl = mgs_slices(M.R);
+  int* __restrict__ nlive = slice_nlive(M);
+  int* __restrict__ list = nlive + 1;
+  if (W > kLiveWords) {
+    for (int c = t; c < C; c += 256) list[c] = c;
+    if (t == 0) *nlive = C;
+    return;
+  }
+  const unsigned* __restrict__ masks = slice_masks(M);
+  for (int wd = t; wd < W; wd += 256) {
+    unsigned m = 0u;
+    for (int i = 0; i < nsl; i++) m |= masks[(size_t)i * W + wd];
+    words[wd] = m;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int o = 0;
+    for (int wd = 0; wd < W; wd++) {
+      offs[wd] = o;
+      o += __popc(words[wd]);
+    }
+    *nlive = o;
+  }
+  __syncthreads();
+  for (int wd = t; wd < W; wd += 256) {
+    unsigned m = words[wd];
+    int o = offs[wd];
+    while (m) {
+      const int i = __ffs(m) - 1;
+      m &= m - 1;
+      list[o++] = 32 * wd + i;
     }
   }
-  if (t == 0) slice_live(M)[b] = n;
+  (void)nmat;
 }
 
 // One column step of the sliced path inside a panel ending at column cend,
@@ -345,12 +398,12 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_kernel(const MuonMat*
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), nlive = slice_live_count(M), ce = min(nlive, cend);
+  const int C = M.C, nsl = mgs_slices(M.R), nlive = *slice_nlive(M), ce = min(nlive, cend);
   if (j >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   const float* __restrict__ Pin = M.red + (size_t)(j & 1) * C * nsl;
   float* __restrict__ Pout = M.red + (size_t)((j + 1) & 1) * C * nsl;
-  const SliceIO io(M, b);
+  const SliceIO io(M, b, slice_list(M));
 
   float q[kSliceEPT], nrm = 1.f;
   if (j >= 0) {
@@ -416,10 +469,10 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_dots_kernel(const Muo
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = *slice_nlive(M);
   if (j1 >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const SliceIO io(M, b);
+  const SliceIO io(M, b, slice_list(M));
   float* __restrict__ pd = slice_dots(M);
   float q[kSlicePanel][kSliceEPT];
 #pragma unroll
@@ -461,7 +514,7 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_dots_kernel(const Muo
 __global__ __launch_bounds__(256) void mgs_slice_reduce_kernel(const MuonMat* __restrict__ mats, int nmat, int j0) {
   const MuonMat& M = mats[blockIdx.y];
   if (M.R <= kMaxPanelR) return;
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = *slice_nlive(M);
   const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int k = p / C, c = p % C;
   if (j1 >= nlive || k >= kSlicePanel || c < j1 || c >= nlive) return;
@@ -481,10 +534,10 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_update_kernel(const M
   int mi, b;
   if (!slice_of(mats, nmat, mi, b)) return;
   const MuonMat& M = mats[mi];
-  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = slice_live_count(M);
+  const int C = M.C, nsl = mgs_slices(M.R), j1 = j0 + kSlicePanel, nlive = *slice_nlive(M);
   if (j1 >= nlive) return;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const SliceIO io(M, b);
+  const SliceIO io(M, b, slice_list(M));
   const float* __restrict__ dd = slice_dot_totals(M);
   float* __restrict__ Pout = M.red + (size_t)(j1 & 1) * C * nsl;
   float q[kSlicePanel][kSliceEPT];
@@ -1032,10 +1085,10 @@ size_t mgs_red_floats(int64_t R, int64_t C) {
   // panel path: the row-compaction tables (header, rank, rows; ints)
   if (R <= kMaxPanelR) return R > kPanelThreads ? (size_t)(kRowHdr + 2 * R) : 0;
   // column partials [2][C][nsl], panel dots [kSlicePanel][C][nsl], their
-  // totals [kSlicePanel][C], and each slice's count of vectors up to its
-  // last nonzero one [nsl] (ints)
-  return R > kMaxPanelR ? (size_t)((2 + kSlicePanel) * C * (int64_t)mgs_slices(R) + kSlicePanel * C + mgs_slices(R))
-                        : 0;
+  // totals [kSlicePanel][C], each slice's mask of nonzero vectors
+  // [nsl][ceil(C / 32)], their count and list [1 + C] (ints)
+  const int64_t nsl = mgs_slices(R);
+  return (size_t)((2 + kSlicePanel) * C * nsl + kSlicePanel * C + nsl * ((C + 31) / 32) + 1 + C);
 }
 
 int launch_muon_gather(const MuonMat* d_mats, int nmat, int64_t max_elems, hipStream_t s) {
@@ -1099,6 +1152,8 @@ int launch_mgs(const MuonMat* d_mats, const MuonMat* h_mats, int nmat, hipStream
   // projections of every later vector (which also start the next panel).
   if (slices > 0) {
     hipLaunchKernelGGL(mgs_slice_live_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat);
+    NSH_LAUNCHED();
+    hipLaunchKernelGGL(mgs_slice_list_kernel, dim3(nmat), dim3(256), 0, ss, d_mats, nmat);
     NSH_LAUNCHED();
     hipLaunchKernelGGL(mgs_slice_kernel, dim3(slices), dim3(kSliceThreads), 0, ss, d_mats, nmat, -1, kSlicePanel);
     NSH_LAUNCHED();
