@@ -359,10 +359,24 @@ __global__ __launch_bounds__(256) void mgs_slice_list_kernel(const MuonMat* __re
     return;
   }
   const unsigned* __restrict__ masks = slice_masks(M);
-  for (int wd = t; wd < W; wd += 256) {
-    unsigned m = 0u;
-    for (int i = 0; i < nsl; i++) m |= masks[(size_t)i * W + wd];
-    words[wd] = m;
+  if (W >= 64) {  // a thread per word
+    for (int wd = t; wd < W; wd += 256) {
+      unsigned m = 0u;
+      for (int i = 0; i < nsl; i++) m |= masks[(size_t)i * W + wd];
+      words[wd] = m;
+    }
+  } else {  // few words (few vectors), many slices: the slices over the threads
+    __shared__ unsigned wpart[4];
+    for (int wd = 0; wd < W; wd++) {
+      unsigned m = 0u;
+      for (int i = t; i < nsl; i += 256) m |= masks[(size_t)i * W + wd];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m |= (unsigned)__shfl_xor((int)m, o, 64);
+      if ((t & 63) == 0) wpart[t >> 6] = m;
+      __syncthreads();
+      if (t == 0) words[wd] = wpart[0] | wpart[1] | wpart[2] | wpart[3];
+      __syncthreads();
+    }
   }
   __syncthreads();
   if (t == 0) {

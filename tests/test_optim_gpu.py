@@ -160,8 +160,8 @@ def test_sliced_orthonormalize_with_zero_vectors(r, c, zero):
     """Zero gradient vectors (a MoE expert without tokens) on the sliced
     path: MGS's +1e-30 guard gives them q = 0, in the panel that holds them
     and as projections of the later panels; everything else as the oracle.
-    Trailing zero vectors (the last 12 of 32, the last 15 of 24) are not
-    processed at all (a slice scan finds the last nonzero vector)."""
+    Zero vectors are not processed at all: the sliced launches run over the
+    list of nonzero ones (here also the last 12 of 32, the last 15 of 24)."""
     print(f"mgs zero vectors {r}x{c} {zero}", flush=True)
     g = synth.normal(r * 5 + c, r * c).reshape(r, c)
     for z in zero:
