@@ -321,15 +321,19 @@ __global__ __launch_bounds__(kSliceThreads) void mgs_slice_live_kernel(const Muo
 #pragma unroll
       for (int u = 0; u < 8; u++) {
         const int c = 32 * wd + i0 + u;
-        if (c < C) io.load(c, x[u]);
+        if (c < C) {
+          io.load(c, x[u]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < kSliceEPT; e++) x[u][e] = 0.f;
+        }
       }
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        const int c = 32 * wd + i0 + u;
         bool nz = false;
 #pragma unroll
         for (int e = 0; e < kSliceEPT; e++) nz |= x[u][e] != 0.f;
-        if (c < C && nz) bits |= 1u << (i0 + u);
+        if (nz) bits |= 1u << (i0 + u);
       }
     }
 #pragma unroll
