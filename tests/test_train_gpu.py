@@ -136,7 +136,8 @@ def test_100_step_loss_curve_matches_reference(curve):
 
 @pytest.mark.parametrize("name,rows", [("c5t", 40), ("mlpt", 17), ("c5s", 64), ("c5s", 2048), ("c5h", 192),
                                        ("c5h", 100), ("moet", 41), ("moet", 300), ("moeb", 4096),
-                                       ("smt", 64), ("drp", 64), ("drp", 29), ("c5w", 400), ("c5w", 130)])
+                                       ("smt", 64), ("drp", 64), ("drp", 29), ("c5w", 400), ("c5w", 130),
+                                       ("embw", 40), ("embw", 400), ("embw", 3000)])
 def test_every_value_of_one_train_step_matches_oracle(name, rows):
     """Each intermediate and gradient of one training step (read back from
     the device by IR value name) against the oracle's value of the same
@@ -151,7 +152,9 @@ def test_every_value_of_one_train_step_matches_oracle(name, rows):
     beyond the bar from the float64 ones.  Networks with operations the
     float64 evaluation does not cover (softmax, dropout, MoE) fall back to
     4x the movement that a random 1-ulp perturbation of the weights causes
-    in the reference, measured at the same bar."""
+    in the reference, measured at the same bar.  embw (a 4096-row
+    embedding) at 40 and 400 tokens runs its Muon MGS on the gradient's
+    live rows only (compacted vectors); at 3000 tokens at full length."""
     ir = helpers.ir_text(name)
     net = oracle.Net(ir)
     seed = 400 + rows
