@@ -1,6 +1,8 @@
 // Multi-head self-attention core over one sequence (S = all rows of the
-// call, as the reference does: codegen.cpp:2224-2235, S = BS), flash-style:
-// no S x S matrix is ever materialised.
+// call, as the reference does: codegen.cpp:2224-2235, S = BS), flash-style
+// for head sizes up to 128: no S x S matrix is ever materialised.  Larger
+// head sizes take the wide path near the end of this file (blocks of query
+// rows' scores materialised, multiplied by the GEMM kernels).
 //
 //   reference arithmetic: ns_attention_fwd, codegen.cpp:1724-1777
 //   (per head: s = (q . k) * 1/sqrt(Dk); row softmax; ctx = P V)
